@@ -1,0 +1,164 @@
+/* q8_rt.h: the Q8_0 weight products of the APL engine's runtime, on one MI355X (gfx950).
+ *
+ * Drop-in for the product half of the reference runtime ABI (src/card/rt.h:61-72) and its
+ * load-time API (src/card/gemv.h:50-67): the same names, argument meanings, shapes and
+ * output layouts. Only pointers and integers cross this interface; no HIP or torch types.
+ *
+ *   y = W x          rt_gemv        W [rows cols] Q8_0, x F32[cols], y F32[rows]
+ *   Y = X W^T        rt_gemm        X F32[t cols] token-major, Y F32[t rows] token-major
+ *
+ * Q8_0 is the GGUF block: per 32 columns of a row, an IEEE binary16 scale d (2 bytes, little
+ * endian) then 32 int8 q; the weight is d*q. A matrix is rows*cols/32 such 34-byte blocks,
+ * row by row (src/card/gemv.c:25, 30-33).
+ *
+ * Weights live in HBM for the life of the process: rt_q8_upload copies a matrix's GGUF rows
+ * to the GPU once and returns the handle that every later product takes as `w`, where the
+ * reference took the address of its repacked form I copy (src/card/engine.c:303-316).
+ * The device form ("form S", below) has the same size as GGUF and as form I, and, like form
+ * I, a prefix of whole 16-row groups is the matrix of those rows: rt_gemv(R, w, 32768, ...)
+ * on the handle of a 151936-row matrix is the product of its first 32768 rows.
+ *
+ * Form S, per 16-row group g (17*cols bytes, at g*17*cols from the handle):
+ *   16*cols bytes   int8 q, row by row (row 16g+r at r*cols), columns in order
+ *   cols bytes      binary16 d, row by row (row 16g+r at 16*cols + r*cols/16), blocks in order
+ *
+ * Shapes: rows % 16 == 0, cols % 32 == 0 (src/card/gemv.h:1-11), as the reference; cols % 4 == 0
+ * also makes every row of x 16-byte aligned. A violation prints the reason and aborts: the
+ * reference's entry points return nothing and do not fail partially.
+ *
+ * Threading: one host thread calls these, as only the card's main thread called the
+ * reference's (src/card/rt.c:31-37, 274-285). The queue is a static of the library: not
+ * reentrant, as the reference's is not (src/card/rt.c:216-226).
+ *
+ * Errors: every HIP call is checked; a failure prints the call and the HIP error and aborts. */
+#ifndef Q8_RT_H
+#define Q8_RT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+struct team;
+struct gemm_chain;
+
+/* The runtime's state, field for field the reference's (src/card/rt.h:19-26), so generated
+ * code that reads R->frame, R->threads or R->last compiles unchanged. rt_init keeps the GPU
+ * context (device, stream, staging buffers) behind `chain`; team and gemm_chain stay NULL. */
+struct rt {
+    struct team *team;
+    char *frame;
+    void *chain;
+    struct gemm_chain *gemm_chain;
+    int threads;
+    int last;
+};
+
+/* ---- init (src/card/rt.h:38-39; rt.c:179-203) */
+
+/* Once, before any product: selects the GPU (Q8_DEVICE, default 0), creates the stream and
+ * the staging buffers. threads is kept in R->threads and otherwise unused: the GPU grid
+ * replaces the team. 0, or -1 when the GPU or its memory is not there. */
+int rt_init(struct rt *R, int threads);
+
+/* Releases the stream, the staging buffers and every uploaded matrix. An addition: the
+ * reference frees nothing before exit. */
+void rt_fini(struct rt *R);
+
+/* ---- products (src/card/rt.h:61-72; rt.c:205-285) */
+
+/* y = W x. x, y host memory: x is copied to HBM, the product runs, y is copied back; returns
+ * when y is valid. (rt.c:205-214) */
+void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
+
+/* Adjacent products: queue up to RT_BATCH, none reading another's result; rt_gemv_go runs them
+ * all and returns when every y is valid. Queued products that share x copy it once.
+ * (rt.h:63-69; rt.c:251-265, 274-285) */
+#define RT_BATCH 8
+void rt_gemv_q(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
+/* Opens the round before x is ready (rt.c:267-272). Nothing to read ahead on the GPU: the
+ * weights are already in HBM. Kept so generated code links; it does nothing. */
+void rt_gemv_open(struct rt *R);
+void rt_gemv_go(struct rt *R);
+
+/* Y = X W^T for t tokens: X [t cols], Y [t rows], both token-major, X rows cols apart
+ * (rt.c:244-249: x_stride = cols). Returns when Y is valid. */
+void rt_gemm(struct rt *R, const void *w, long rows, long cols, const float *x, long t, float *y);
+/* The same, queued into the round of rt_gemv_go (rt.c:260-265). */
+void rt_gemm_q(struct rt *R, const void *w, long rows, long cols, const float *x, long t, float *y);
+
+/* ---- load time (src/card/gemv.h:50-67; gemv.c:13-52; engine.c:303-316) */
+
+/* Bytes of the repacked form: rows/16 * cols/32 * 544, which is also the GGUF size. (gemv.c:13) */
+long gemv_i_bytes(long rows, long cols);
+
+/* GGUF Q8_0 rows (rows*cols/32 blocks of 34 B, host memory) into form S at out (host memory,
+ * gemv_i_bytes(rows, cols) bytes; out must not overlap q8). The host-side analogue of the
+ * reference's repack into form I (gemv.c:23-40), for callers that stage weights themselves. */
+void gemv_i_repack(const uint8_t *q8, long rows, long cols, void *out);
+
+/* GGUF Q8_0 rows in host memory to HBM, repacked there into form S by the GPU: the handle for
+ * `w`. Call once per distinct tensor (tied tensors share a handle, engine.c:307-310). The
+ * host buffer may be freed on return. NULL when HBM is full. */
+const void *rt_q8_upload(struct rt *R, const uint8_t *q8, long rows, long cols);
+/* The same for a matrix already in form S in host memory (gemv_i_repack's output). */
+const void *rt_q8_upload_packed(struct rt *R, const void *packed, long rows, long cols);
+/* Frees an uploaded matrix. */
+void rt_q8_free(struct rt *R, const void *w);
+
+/* ---- activations already in HBM (additions: no copies, stream-ordered, no wait)
+ *
+ * x, y are device addresses (from rt_dev_alloc, or any HIP allocation on the device). The
+ * products are enqueued on the runtime's stream in call order, so a product that reads
+ * another's y sees it; rt_dev_sync waits for all of them. These are what a caller that keeps
+ * its activations in HBM uses, and what the throughput figures time. */
+void rt_gemv_dev(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
+/* Y = X W^T, t tokens (1..64), X rows x_stride floats apart (x_stride >= cols, % 4 == 0). */
+void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* The FFN's fused pair: Y[k] = SiLU(G[k]) * U[k] with G = X Wg^T and U = X Wu^T, both [rows cols],
+ * x read once for both; SiLU(g) = g / (1 + exp(-g)) (src/apl/qwen35.apl:38, 125). t tokens. */
+void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* Device memory for activations, and copies to and from it on the runtime's stream. */
+void *rt_dev_alloc(struct rt *R, long bytes);
+void rt_dev_free(struct rt *R, void *p);
+void rt_dev_upload(struct rt *R, void *dst, const void *src, long bytes);
+void rt_dev_download(struct rt *R, void *dst, const void *src, long bytes);
+void rt_dev_sync(struct rt *R);
+
+/* ---- host-side tests and benchmarks (additions) */
+
+/* Synthetic GGUF Q8_0 rows written on the GPU at dst (device, rows*cols/32*34 bytes): q uniform
+ * integers in [-127, 127]; d = binary16(|N(0, sigma)| / 127) when dist == 0, or
+ * binary16(lognormal(mu, sigma)) when dist == 1. A function of (seed, row, block) only. */
+void rt_q8_fill_dev(struct rt *R, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma);
+/* Form S from GGUF rows, both in HBM (the repack rt_q8_upload runs). */
+void rt_q8_repack_dev(struct rt *R, const void *q8_dev, long rows, long cols, void *out_dev);
+/* F32 N(0,1) values on the GPU: a function of (seed, index) only. */
+void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed);
+
+/* The product kernels' primitive conversions on the GPU, lane by lane: o8[i] = fma(x8[i],
+ * (float)q[i], c8[i]) with the int8 convert of the weights (n8 % 4 == 0), of[i] = fma(xf[i],
+ * (float)binary16 h[i], cf[i]) with the scale convert; all device arrays. The reference's
+ * gate 2.1 s8 and f16 sets (src/gate/upconv_kernel.c:18-22, 51-55) hash these. */
+void rt_prims_dev(struct rt *R, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h, const float *xf,
+                  const float *cf, float *of, long nf);
+
+/* Product kernels: 0 = the fast kernels (default), 1 = the reference-order kernels, whose every
+ * y is bit-identical to the reference's F32 host path (src/card/gemv.c:165-193 at one thread;
+ * gemm.c:20-23 per token). Returns the previous mode. Q8_EXACT=1 in the environment sets 1. */
+int rt_set_exact(struct rt *R, int exact);
+
+/* Event timing on the runtime's stream: rt_timer_start, then rt_timer_stop returns the
+ * milliseconds between them (waits for the stream). */
+void rt_timer_start(struct rt *R);
+float rt_timer_stop(struct rt *R);
+
+/* The device's name and its count of compute units, for reports. */
+void rt_device_info(struct rt *R, char *name, long name_len, int *cus);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,169 @@
+"""Python view of libq8rt.so, the MI355X Q8_0 weight products (include/q8_rt.h).
+
+The product is the C-ABI: this module binds it with ctypes for the tests and the benchmark,
+names every symbol the header declares, and wraps a `struct rt` in `Runtime`. It computes
+nothing itself: every product runs in the HIP kernels of libq8rt.so, and a missing library
+is an error (RuntimeError), never a fallback.
+
+Reference interface mirrored: src/card/rt.h:19-26 (struct rt), 38-39 (rt_init), 61-72
+(rt_gemv, rt_gemv_q, rt_gemv_open, rt_gemv_go, rt_gemm, rt_gemm_q); src/card/gemv.h:50-57
+(gemv_i_bytes, gemv_i_repack).
+"""
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq8rt.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "q8_rt.h")
+
+_c = ctypes
+_vp, _long, _int, _f32p, _u64 = _c.c_void_p, _c.c_long, _c.c_int, _c.c_void_p, _c.c_uint64
+
+
+class Rt(_c.Structure):
+    """struct rt, field for field (src/card/rt.h:19-26)."""
+
+    _fields_ = [("team", _vp), ("frame", _c.c_char_p), ("chain", _vp), ("gemm_chain", _vp), ("threads", _int), ("last", _int)]
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "rt_init": (_int, [_vp, _int]),
+    "rt_fini": (None, [_vp]),
+    "rt_gemv": (None, [_vp, _vp, _long, _long, _vp, _vp]),
+    "rt_gemv_q": (None, [_vp, _vp, _long, _long, _vp, _vp]),
+    "rt_gemv_open": (None, [_vp]),
+    "rt_gemv_go": (None, [_vp]),
+    "rt_gemm": (None, [_vp, _vp, _long, _long, _vp, _long, _vp]),
+    "rt_gemm_q": (None, [_vp, _vp, _long, _long, _vp, _long, _vp]),
+    "gemv_i_bytes": (_long, [_long, _long]),
+    "gemv_i_repack": (None, [_vp, _long, _long, _vp]),
+    "rt_q8_upload": (_vp, [_vp, _vp, _long, _long]),
+    "rt_q8_upload_packed": (_vp, [_vp, _vp, _long, _long]),
+    "rt_q8_free": (None, [_vp, _vp]),
+    "rt_gemv_dev": (None, [_vp, _vp, _long, _long, _vp, _vp]),
+    "rt_gemm_dev": (None, [_vp, _vp, _long, _long, _vp, _long, _long, _vp]),
+    "rt_gemv_swiglu_dev": (None, [_vp, _vp, _vp, _long, _long, _vp, _long, _long, _vp]),
+    "rt_dev_alloc": (_vp, [_vp, _long]),
+    "rt_dev_free": (None, [_vp, _vp]),
+    "rt_dev_upload": (None, [_vp, _vp, _vp, _long]),
+    "rt_dev_download": (None, [_vp, _vp, _vp, _long]),
+    "rt_dev_sync": (None, [_vp]),
+    "rt_q8_fill_dev": (None, [_vp, _vp, _long, _long, _u64, _int, _c.c_float, _c.c_float]),
+    "rt_q8_repack_dev": (None, [_vp, _vp, _long, _long, _vp]),
+    "rt_f32_fill_dev": (None, [_vp, _vp, _long, _u64]),
+    "rt_prims_dev": (None, [_vp, _vp, _vp, _vp, _vp, _long, _vp, _vp, _vp, _vp, _long]),
+    "rt_set_exact": (_int, [_vp, _int]),
+    "rt_timer_start": (None, [_vp]),
+    "rt_timer_stop": (_c.c_float, [_vp]),
+    "rt_device_info": (None, [_vp, _c.c_char_p, _long, _c.POINTER(_int)]),
+}
+
+
+def header_symbols(path=HEADER):
+    """Every function name include/q8_rt.h declares."""
+    text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(\w+)\s*\(", text, flags=re.M)) - {"defined"})
+
+
+_lib = None
+
+
+def load():
+    """The library, its signatures set. RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run `make -C {HERE}` or __graft_entry__.build()")
+    lib = _c.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def ptr(a):
+    """The address of a numpy array's data (or an int address) as a c_void_p."""
+    if isinstance(a, int):
+        return _c.c_void_p(a)
+    if a is None:
+        return _c.c_void_p(0)
+    return _c.c_void_p(a.ctypes.data)
+
+
+class Runtime:
+    """One `struct rt` with rt_init done; the GPU context lives until close()."""
+
+    def __init__(self, threads=1):
+        self.lib = load()
+        self.rt = Rt()
+        if self.lib.rt_init(_c.byref(self.rt), threads) != 0:
+            raise RuntimeError("rt_init failed: no GPU visible, or no memory for the runtime")
+        self.R = _c.byref(self.rt)
+
+    def close(self):
+        if self.rt.chain:
+            self.lib.rt_fini(self.R)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- the reference's entry points, host arrays (numpy float32, C-contiguous)
+    def upload(self, q8, rows, cols):
+        h = self.lib.rt_q8_upload(self.R, ptr(q8), rows, cols)
+        if not h:
+            raise MemoryError("rt_q8_upload: HBM is full")
+        return h
+
+    def gemv(self, w, rows, cols, x, y):
+        self.lib.rt_gemv(self.R, _c.c_void_p(w), rows, cols, ptr(x), ptr(y))
+
+    def gemm(self, w, rows, cols, x, t, y):
+        self.lib.rt_gemm(self.R, _c.c_void_p(w), rows, cols, ptr(x), t, ptr(y))
+
+    def gemv_q(self, w, rows, cols, x, y):
+        self.lib.rt_gemv_q(self.R, _c.c_void_p(w), rows, cols, ptr(x), ptr(y))
+
+    def gemm_q(self, w, rows, cols, x, t, y):
+        self.lib.rt_gemm_q(self.R, _c.c_void_p(w), rows, cols, ptr(x), t, ptr(y))
+
+    def gemv_open(self):
+        self.lib.rt_gemv_open(self.R)
+
+    def gemv_go(self):
+        self.lib.rt_gemv_go(self.R)
+
+    def set_exact(self, on):
+        return self.lib.rt_set_exact(self.R, 1 if on else 0)
+
+    # ---- device memory
+    def alloc(self, nbytes):
+        p = self.lib.rt_dev_alloc(self.R, int(nbytes))
+        if not p:
+            raise MemoryError(f"rt_dev_alloc({nbytes})")
+        return p
+
+    def free(self, p):
+        self.lib.rt_dev_free(self.R, _c.c_void_p(p))
+
+    def to_dev(self, dst, a):
+        self.lib.rt_dev_upload(self.R, _c.c_void_p(dst), ptr(a), a.nbytes)
+
+    def from_dev(self, a, src):
+        self.lib.rt_dev_download(self.R, ptr(a), _c.c_void_p(src), a.nbytes)
+
+    def sync(self):
+        self.lib.rt_dev_sync(self.R)
+
+    def device_info(self):
+        name = _c.create_string_buffer(256)
+        cus = _int(0)
+        self.lib.rt_device_info(self.R, name, 256, _c.byref(cus))
+        return name.value.decode(), cus.value

@@ -1,0 +1,90 @@
+/* q8_device.h: what every kernel of the library shares: the form S addressing, the exact
+ * conversions, the reductions, and the launchers' declarations (host side).
+ *
+ * Form S (include/q8_rt.h), per 16-row group g at g*17*cols bytes:
+ *   16*cols int8 q, row by row (row 16g+r at r*cols);
+ *   then cols bytes of binary16 d, row by row (row 16g+r at 16*cols + r*cols/16).
+ * Like the reference's form I (src/card/gemv.c:23-40) it is 17/16 bytes per weight and a
+ * 16-row group holds everything of its rows, so a prefix of groups is a smaller matrix. Unlike
+ * form I, a row's 32 weights of a block lie in column order, contiguous: a lane's 16-byte load
+ * is 16 columns of one row, and 64 lanes read 1 KiB of one row at once. */
+#ifndef Q8_DEVICE_H
+#define Q8_DEVICE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define Q8_GROUP 16
+#define Q8_BLOCK 32
+#define Q8_BLOCK_BYTES 34
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+
+/* bytes from the handle to the start of row r's int8 weights / binary16 scales */
+__device__ __forceinline__ size_t q8s_row_q(long r, long cols)
+{
+    return (size_t)(r >> 4) * 17u * (size_t)cols + (size_t)(r & 15) * (size_t)cols;
+}
+__device__ __forceinline__ size_t q8s_row_d(long r, long cols)
+{
+    return (size_t)(r >> 4) * 17u * (size_t)cols + 16u * (size_t)cols + (size_t)(r & 15) * (size_t)(cols / 16);
+}
+
+/* byte k of w as a signed integer, to binary32: exact (|q| <= 128). One v_cvt_f32_i32 with an
+ * SDWA sign-extended byte select on gfx950. */
+__device__ __forceinline__ float q8_s8(uint32_t w, int k)
+{
+    return (float)(int8_t)(uint8_t)(w >> (8 * k));
+}
+
+/* binary16 to binary32: v_cvt_f32_f16, exact for every pattern (subnormals kept: the f16
+ * denormal mode is on for HIP kernels). */
+__device__ __forceinline__ float q8_half(uint16_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+/* sum over the 64 lanes, the same pairing on every call: the result in every lane */
+__device__ __forceinline__ float q8_wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+/* SiLU(g) * u (src/apl/qwen35.apl:38; docs/model.md:29: Sig = 1 / (1 + exp(min(700, -g)))):
+ * in binary32 exp(min(700, -g)) overflows to inf for -g > 88.7 exactly as exp(-g) does, so
+ * the clamp changes nothing and is left out. */
+__device__ __forceinline__ float q8_swiglu(float g, float u)
+{
+    return g / (1.0f + __expf(-g)) * u;
+}
+#endif
+
+/* ---- launchers (q8_kernels.hip), all asynchronous on `stream` */
+#ifdef __cplusplus
+struct ihipStream_t;
+typedef struct ihipStream_t *q8_stream_t;
+
+/* Y = X W^T, t tokens, the fast kernels; W form S. w1 != NULL: the fused pair, Y = SiLU(X W0^T) * (X W1^T). */
+void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* The reference's order, every y bit-identical to the reference's F32 host path. */
+void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* Y = X W^T for 5 <= t <= 64 on the matrix cores. */
+void q8_launch_gemm(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
+void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
+/* GGUF Q8_0 rows to form S, both device. */
+void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, void *out);
+/* Synthetic GGUF rows and F32 values on the device. */
+void q8_launch_fill(q8_stream_t stream, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma);
+void q8_launch_fill_f32(q8_stream_t stream, float *dst, long n, uint64_t seed);
+/* The primitive conversions of the product kernels, lane by lane (the reference's gate 2.1
+ * s8 and f16 sets, src/gate/upconv_kernel.c:18-57). */
+void q8_launch_prims(q8_stream_t stream, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h,
+                     const float *xf, const float *cf, float *of, long nf);
+#endif
+
+#endif

@@ -1,0 +1,310 @@
+/* q8_kernels.hip: the Q8_0 product kernels for gfx950 and their launchers.
+ *
+ *   gemv_s      decode, t = 1..4 tokens: HBM-bound (1.88 flop/B). Each wave owns RW rows
+ *               of one 16-row group and the whole of K; each lane takes 16-column units
+ *               (one 16-byte load of one row) 64 units apart, so a wave reads 1 KiB of a row
+ *               per load. Per unit: 16 exact int8->f32 converts, shared by the t tokens, a
+ *               16-step fma chain per token, then acc = fma(s, d, acc) with the unit's
+ *               binary16 block scale. One fixed-order sum over the wave's lanes at the end.
+ *               With a second matrix the pair shares every load of x and ends in
+ *               SiLU(g) * u (the FFN's gate and up, src/apl/qwen35.apl:125).
+ *   exact_s     the reference's order (src/card/gemv.c:166-193; gemm.c:20-23 per token): one
+ *               lane per (token, row), T from +0 by 32 fma in column order, then
+ *               acc = fma(T, d, acc). Bit-identical to the reference's F32 host path.
+ *   repack_s    GGUF rows to form S.
+ *   fill_*      synthetic weights and activations, a function of (seed, index) only.
+ *   prims       the conversions above, lane by lane, for the known-answer gates. */
+#include <hip/hip_runtime.h>
+
+#include "q8_device.h"
+
+/* ---------------------------------------------------------------- decode GEMV */
+
+#define GEMV_WAVES 4 /* waves per workgroup */
+
+template <int MT, int RW, int PAIR>
+__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_s(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
+                                                          const float *__restrict__ x, long x_stride, float *__restrict__ y)
+{
+    const int lane = threadIdx.x & 63;
+    const long r0 = ((long)blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6)) * RW;
+    if (r0 >= rows)
+        return;
+    const long units = cols / 16; /* even: cols % 32 == 0 */
+    const uint8_t *wq[PAIR + 1][RW];
+    const uint16_t *wd[PAIR + 1][RW];
+#pragma unroll
+    for (int p = 0; p <= PAIR; p++) {
+        const uint8_t *w = p ? w1 : w0;
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            wq[p][r] = w + q8s_row_q(r0 + r, cols);
+            wd[p][r] = (const uint16_t *)(w + q8s_row_d(r0 + r, cols));
+        }
+    }
+    float acc[PAIR + 1][RW][MT];
+#pragma unroll
+    for (int p = 0; p <= PAIR; p++)
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                acc[p][r][m] = 0.0f;
+
+    for (long u = lane; u < units; u += 64) {
+        /* every load of the step first: RW (x2) rows of weights, their scales, x */
+        uint4 q[PAIR + 1][RW];
+        uint16_t dh[PAIR + 1][RW];
+#pragma unroll
+        for (int p = 0; p <= PAIR; p++)
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+                q[p][r] = *(const uint4 *)(wq[p][r] + 16 * u);
+                dh[p][r] = wd[p][r][u >> 1];
+            }
+        float4 xv[MT][4];
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                xv[m][c] = *(const float4 *)(x + m * x_stride + 16 * u + 4 * c);
+#pragma unroll
+        for (int p = 0; p <= PAIR; p++)
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+                const uint32_t qw[4] = {q[p][r].x, q[p][r].y, q[p][r].z, q[p][r].w};
+                float wf[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    wf[j] = q8_s8(qw[j >> 2], j & 3);
+                const float d = q8_half(dh[p][r]);
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    const float xs[16] = {xv[m][0].x, xv[m][0].y, xv[m][0].z, xv[m][0].w, xv[m][1].x, xv[m][1].y, xv[m][1].z, xv[m][1].w,
+                                          xv[m][2].x, xv[m][2].y, xv[m][2].z, xv[m][2].w, xv[m][3].x, xv[m][3].y, xv[m][3].z, xv[m][3].w};
+                    float s = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 16; j++)
+                        s = __builtin_fmaf(wf[j], xs[j], s);
+                    acc[p][r][m] = __builtin_fmaf(s, d, acc[p][r][m]);
+                }
+            }
+    }
+#pragma unroll
+    for (int p = 0; p <= PAIR; p++)
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                acc[p][r][m] = q8_wave_sum(acc[p][r][m]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                y[m * rows + r0 + r] = PAIR ? q8_swiglu(acc[0][r][m], acc[PAIR][r][m]) : acc[0][r][m];
+    }
+}
+
+template <int MT, int RW, int PAIR>
+static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y)
+{
+    const long waves = rows / RW;
+    const dim3 grid((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES));
+    gemv_s<MT, RW, PAIR><<<grid, 64 * GEMV_WAVES, 0, s>>>((const uint8_t *)w0, (const uint8_t *)w1, rows, cols, x, xs, y);
+}
+
+template <int RW, int PAIR>
+static void gemv_t(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y)
+{
+    switch (t) {
+    case 1: gemv_go<1, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    case 2: gemv_go<2, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    case 3: gemv_go<3, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    default: gemv_go<4, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    }
+}
+
+void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y)
+{
+    hipStream_t s = (hipStream_t)stream;
+    /* at most 4 tokens a launch; more go token slice by token slice */
+    for (long k = 0; k < t; k += 4) {
+        const long n = t - k < 4 ? t - k : 4;
+        if (w1)
+            gemv_t<4, 1>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
+        else
+            gemv_t<4, 0>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
+    }
+}
+
+/* ---------------------------------------------------------------- the reference's order */
+
+__global__ __launch_bounds__(256) void exact_s(const uint8_t *__restrict__ w, long rows, long cols, const float *__restrict__ x, long x_stride, long t,
+                                               float *__restrict__ y)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * t)
+        return;
+    const long r = i % rows, m = i / rows;
+    const uint8_t *q = w + q8s_row_q(r, cols);
+    const uint16_t *d = (const uint16_t *)(w + q8s_row_d(r, cols));
+    const float *xm = x + m * x_stride;
+    float acc = 0.0f;
+    for (long b = 0; b < cols / Q8_BLOCK; b++) {
+        float tb = 0.0f;
+        for (int h = 0; h < 2; h++) {
+            const uint4 v = *(const uint4 *)(q + 32 * b + 16 * h);
+            const uint32_t qw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                tb = __builtin_fmaf(q8_s8(qw[j >> 2], j & 3), xm[32 * b + 16 * h + j], tb);
+        }
+        acc = __builtin_fmaf(tb, q8_half(d[b]), acc);
+    }
+    y[m * rows + r] = acc;
+}
+
+void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y)
+{
+    const long n = rows * t;
+    exact_s<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)w, rows, cols, x, x_stride, t, y);
+}
+
+__global__ __launch_bounds__(256) void swiglu_ew(const float *__restrict__ g, const float *__restrict__ u, long n, float *__restrict__ y)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        y[i] = q8_swiglu(g[i], u[i]);
+}
+
+void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y)
+{
+    swiglu_ew<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>(g, u, n, y);
+}
+
+/* ---------------------------------------------------------------- GGUF -> form S */
+
+/* One thread per block of 32 weights: the 34 GGUF bytes (2-byte aligned: 34 = 2 * 17) in, 32
+ * int8 to the row's q (32-byte aligned: two 16-byte stores) and the scale to the row's d. */
+__global__ __launch_bounds__(256) void repack_s(const uint8_t *__restrict__ q8, long rows, long cols, uint8_t *__restrict__ out)
+{
+    const long nb = cols / Q8_BLOCK;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nb)
+        return;
+    const long r = i / nb, b = i % nb;
+    const uint16_t *src = (const uint16_t *)(q8 + i * Q8_BLOCK_BYTES);
+    uint16_t h[17];
+#pragma unroll
+    for (int k = 0; k < 17; k++)
+        h[k] = src[k];
+    uint32_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        v[k] = (uint32_t)h[1 + 2 * k] | (uint32_t)h[2 + 2 * k] << 16;
+    uint4 *dq = (uint4 *)(out + q8s_row_q(r, cols) + Q8_BLOCK * b);
+    dq[0] = make_uint4(v[0], v[1], v[2], v[3]);
+    dq[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    ((uint16_t *)(out + q8s_row_d(r, cols)))[b] = h[0];
+}
+
+void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, void *out)
+{
+    const long n = rows * (cols / Q8_BLOCK);
+    repack_s<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)q8, rows, cols, (uint8_t *)out);
+}
+
+/* ---------------------------------------------------------------- synthetic inputs */
+
+/* splitmix64's finaliser: a bijection of 64-bit words with full avalanche */
+__device__ __forceinline__ uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t hash3(uint64_t seed, uint64_t a, uint64_t b)
+{
+    return mix64(mix64(seed ^ mix64(a + 0x9e3779b97f4a7c15ull)) + b);
+}
+
+/* uniform in (0, 1]: 24 random bits */
+__device__ __forceinline__ float unit_open(uint32_t v) { return ((float)(v >> 8) + 1.0f) * (1.0f / 16777216.0f); }
+
+/* N(0,1) by Box-Muller from one 64-bit word */
+__device__ __forceinline__ float normal01(uint64_t h)
+{
+    const float u1 = unit_open((uint32_t)h), u2 = unit_open((uint32_t)(h >> 32));
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.2831853071795864f * u2);
+}
+
+/* One thread per block: scale from hash(seed, row, block), then 32 q uniform in [-127, 127]
+ * from 16 more words (the high 32 bits times 255, shifted: bias below 2^-24). */
+__global__ __launch_bounds__(256) void fill_q8(uint8_t *__restrict__ dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma)
+{
+    const long nb = cols / Q8_BLOCK;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nb)
+        return;
+    const long r = i / nb, b = i % nb;
+    const float z = normal01(hash3(seed, (uint64_t)r, (uint64_t)b * 64u));
+    const float dv = dist == 0 ? fabsf(z) * sigma / 127.0f : expf(mu + sigma * z);
+    const _Float16 d16 = (_Float16)dv;
+    uint16_t out[17];
+    out[0] = __builtin_bit_cast(uint16_t, d16);
+    for (int k = 0; k < 16; k++) {
+        const uint64_t h = hash3(seed, (uint64_t)r, (uint64_t)b * 64u + 1u + (uint64_t)k);
+        const int q0 = (int)(((h >> 32) * 255u) >> 32) - 127;
+        const int q1 = (int)(((h & 0xffffffffu) * 255u) >> 32) - 127;
+        out[1 + k] = (uint16_t)((uint8_t)(int8_t)q0 | (uint16_t)(uint8_t)(int8_t)q1 << 8);
+    }
+    uint16_t *p = (uint16_t *)(dst + i * Q8_BLOCK_BYTES);
+    for (int k = 0; k < 17; k++)
+        p[k] = out[k];
+}
+
+void q8_launch_fill(q8_stream_t stream, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma)
+{
+    const long n = rows * (cols / Q8_BLOCK);
+    fill_q8<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>((uint8_t *)dst, rows, cols, seed, dist, mu, sigma);
+}
+
+__global__ __launch_bounds__(256) void fill_f32(float *__restrict__ dst, long n, uint64_t seed)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        dst[i] = normal01(hash3(seed, 0x5eedull, (uint64_t)i));
+}
+
+void q8_launch_fill_f32(q8_stream_t stream, float *dst, long n, uint64_t seed)
+{
+    fill_f32<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>(dst, n, seed);
+}
+
+/* ---------------------------------------------------------------- primitive gates */
+
+/* o8[i] = fma(x8[i], s8(q[i]), c8[i]) through the product kernels' byte convert (four bytes
+ * a word, as they load them); of[i] = fma(xf[i], half(h[i]), cf[i]). n8 % 4 == 0. */
+__global__ __launch_bounds__(256) void prims(const int8_t *__restrict__ q, const float *__restrict__ x8, const float *__restrict__ c8, float *__restrict__ o8,
+                                             long n8, const uint16_t *__restrict__ h, const float *__restrict__ xf, const float *__restrict__ cf,
+                                             float *__restrict__ of, long nf)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (4 * i < n8) {
+        const uint32_t w = ((const uint32_t *)q)[i];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            o8[4 * i + k] = __builtin_fmaf(x8[4 * i + k], q8_s8(w, k), c8[4 * i + k]);
+    }
+    if (i < nf)
+        of[i] = __builtin_fmaf(xf[i], q8_half(h[i]), cf[i]);
+}
+
+void q8_launch_prims(q8_stream_t stream, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h, const float *xf,
+                     const float *cf, float *of, long nf)
+{
+    const long n = nf > n8 / 4 ? nf : n8 / 4;
+    prims<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>(q, x8, c8, o8, n8, h, xf, cf, of, nf);
+}

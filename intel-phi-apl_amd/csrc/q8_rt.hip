@@ -1,0 +1,521 @@
+/* q8_rt.hip: the C-ABI of include/q8_rt.h over HIP: the GPU context behind struct rt, weight
+ * upload, the queue of a round, and the host-pointer and device-pointer products.
+ *
+ * The reference's products ran on the card's team out of the card's memory (src/card/rt.c:
+ * 205-285); here the weights are HBM-resident handles and a round is: every distinct x into
+ * one pinned staging buffer, one copy to HBM, one launch per product on the runtime's stream,
+ * one copy of every y back, one wait. */
+#include <hip/hip_runtime.h>
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <unordered_map>
+
+#include "../../include/q8_rt.h"
+#include "q8_device.h"
+
+#define HIPCHECK(call)                                                                                                 \
+    do {                                                                                                               \
+        hipError_t e_ = (call);                                                                                        \
+        if (e_ != hipSuccess) {                                                                                        \
+            fprintf(stderr, "q8_rt: %s failed: %s (%s:%d)\n", #call, hipGetErrorString(e_), __FILE__, __LINE__);       \
+            abort();                                                                                                   \
+        }                                                                                                              \
+    } while (0)
+
+static void fail(const char *fn, const char *why)
+{
+    fprintf(stderr, "q8_rt: %s: %s\n", fn, why);
+    abort();
+}
+
+namespace {
+
+struct matrix {
+    long rows, cols;
+};
+
+struct job {
+    const void *w;
+    long rows, cols, t;
+    const float *x;
+    float *y;
+    size_t x_off, y_off; /* floats, in the staging buffers */
+};
+
+struct ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    int exact = 0;
+    /* staging for the host-pointer products: pinned host and device, in floats */
+    float *hx = nullptr, *hy = nullptr, *dx = nullptr, *dy = nullptr;
+    size_t x_cap = 0, y_cap = 0;
+    /* scratch for the exact fused pair: G and U */
+    float *scratch = nullptr;
+    size_t scratch_cap = 0;
+    std::unordered_map<const void *, matrix> weights;
+    job queue[RT_BATCH];
+    int queued = 0;
+};
+
+ctx *get(struct rt *R, const char *fn)
+{
+    if (!R || !R->chain)
+        fail(fn, "rt_init has not run on this struct rt");
+    return (ctx *)R->chain;
+}
+
+void check_shape(ctx *c, const char *fn, const void *w, long rows, long cols)
+{
+    if (!w)
+        fail(fn, "w is NULL");
+    if (rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK) {
+        fprintf(stderr, "q8_rt: %s: rows %ld must be a positive multiple of 16 and cols %ld of 32\n", fn, rows, cols);
+        abort();
+    }
+    auto it = c->weights.find(w);
+    if (it != c->weights.end() && (it->second.cols != cols || rows > it->second.rows)) {
+        fprintf(stderr, "q8_rt: %s: w was uploaded as %ld x %ld, used as %ld x %ld (only a prefix of whole 16-row groups may be used)\n", fn,
+                it->second.rows, it->second.cols, rows, cols);
+        abort();
+    }
+}
+
+void check_dev_ptr(const char *fn, const void *p, const char *what)
+{
+    if (!p || ((uintptr_t)p & 15)) {
+        fprintf(stderr, "q8_rt: %s: %s must be a 16-byte aligned device address\n", fn, what);
+        abort();
+    }
+}
+
+void grow_pinned(float **p, size_t *cap_unused, size_t n)
+{
+    (void)cap_unused;
+    if (*p)
+        HIPCHECK(hipHostFree(*p));
+    HIPCHECK(hipHostMalloc((void **)p, n * sizeof(float), hipHostMallocDefault));
+}
+
+void reserve_staging(ctx *c, size_t nx, size_t ny)
+{
+    if (nx > c->x_cap) {
+        size_t n = nx + nx / 2 + 4096;
+        grow_pinned(&c->hx, nullptr, n);
+        if (c->dx)
+            HIPCHECK(hipFree(c->dx));
+        HIPCHECK(hipMalloc((void **)&c->dx, n * sizeof(float)));
+        c->x_cap = n;
+    }
+    if (ny > c->y_cap) {
+        size_t n = ny + ny / 2 + 4096;
+        grow_pinned(&c->hy, nullptr, n);
+        if (c->dy)
+            HIPCHECK(hipFree(c->dy));
+        HIPCHECK(hipMalloc((void **)&c->dy, n * sizeof(float)));
+        c->y_cap = n;
+    }
+}
+
+float *reserve_scratch(ctx *c, size_t n)
+{
+    if (n > c->scratch_cap) {
+        if (c->scratch)
+            HIPCHECK(hipFree(c->scratch));
+        HIPCHECK(hipMalloc((void **)&c->scratch, n * sizeof(float)));
+        c->scratch_cap = n;
+    }
+    return c->scratch;
+}
+
+void launched(const char *what)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "q8_rt: launch of %s failed: %s\n", what, hipGetErrorString(e));
+        abort();
+    }
+}
+
+/* Y = X W^T (w1 NULL) or SiLU(X W0^T) * (X W1^T), device pointers, on the stream */
+void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y)
+{
+    q8_stream_t s = (q8_stream_t)c->stream;
+    if (c->exact) {
+        if (!w1) {
+            q8_launch_exact(s, w0, rows, cols, x, xs, t, y);
+        } else {
+            float *g = reserve_scratch(c, (size_t)(2 * rows * t));
+            q8_launch_exact(s, w0, rows, cols, x, xs, t, g);
+            q8_launch_exact(s, w1, rows, cols, x, xs, t, g + rows * t);
+            q8_launch_swiglu_ew(s, g, g + rows * t, rows * t, y);
+        }
+        launched("the reference-order product");
+        return;
+    }
+    if (t <= 4)
+        q8_launch_gemv(s, w0, w1, rows, cols, x, xs, t, y);
+    else
+        q8_launch_gemm(s, w0, w1, rows, cols, x, xs, t, y);
+    launched("the product");
+}
+
+/* A round over host pointers: distinct x staged once, every product, every y back, one wait. */
+void run_round(ctx *c, job *jobs, int n)
+{
+    size_t nx = 0, ny = 0;
+    for (int i = 0; i < n; i++) {
+        job &j = jobs[i];
+        const size_t xlen = (size_t)(j.t * j.cols);
+        j.x_off = (size_t)-1;
+        for (int k = 0; k < i; k++)
+            if (jobs[k].x == j.x && (size_t)(jobs[k].t * jobs[k].cols) == xlen) {
+                j.x_off = jobs[k].x_off;
+                break;
+            }
+        if (j.x_off == (size_t)-1) {
+            j.x_off = nx;
+            nx += (xlen + 63) / 64 * 64;
+        }
+        j.y_off = ny;
+        ny += ((size_t)(j.t * j.rows) + 63) / 64 * 64;
+    }
+    reserve_staging(c, nx, ny);
+    for (int i = 0; i < n; i++) {
+        const job &j = jobs[i];
+        bool first = true;
+        for (int k = 0; k < i; k++)
+            if (jobs[k].x_off == j.x_off)
+                first = false;
+        if (first)
+            memcpy(c->hx + j.x_off, j.x, sizeof(float) * (size_t)(j.t * j.cols));
+    }
+    HIPCHECK(hipMemcpyAsync(c->dx, c->hx, nx * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    for (int i = 0; i < n; i++) {
+        const job &j = jobs[i];
+        product(c, j.w, nullptr, j.rows, j.cols, c->dx + j.x_off, j.cols, j.t, c->dy + j.y_off);
+    }
+    HIPCHECK(hipMemcpyAsync(c->hy, c->dy, ny * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    for (int i = 0; i < n; i++)
+        memcpy(jobs[i].y, c->hy + jobs[i].y_off, sizeof(float) * (size_t)(jobs[i].t * jobs[i].rows));
+}
+
+} // namespace
+
+extern "C" {
+
+int rt_init(struct rt *R, int threads)
+{
+    if (!R)
+        return -1;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count < 1)
+        return -1;
+    const char *dev = getenv("Q8_DEVICE");
+    const int device = dev ? atoi(dev) : 0;
+    if (device < 0 || device >= count)
+        return -1;
+    if (hipSetDevice(device) != hipSuccess)
+        return -1;
+    ctx *c = new ctx;
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess || hipEventCreate(&c->ev0) != hipSuccess ||
+        hipEventCreate(&c->ev1) != hipSuccess) {
+        delete c;
+        return -1;
+    }
+    const char *ex = getenv("Q8_EXACT");
+    c->exact = ex && atoi(ex) != 0;
+    R->team = nullptr;
+    R->gemm_chain = nullptr;
+    R->chain = c;
+    R->threads = threads;
+    return 0;
+}
+
+void rt_fini(struct rt *R)
+{
+    if (!R || !R->chain)
+        return;
+    ctx *c = (ctx *)R->chain;
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    for (auto &kv : c->weights)
+        HIPCHECK(hipFree((void *)kv.first));
+    if (c->hx)
+        HIPCHECK(hipHostFree(c->hx));
+    if (c->hy)
+        HIPCHECK(hipHostFree(c->hy));
+    if (c->dx)
+        HIPCHECK(hipFree(c->dx));
+    if (c->dy)
+        HIPCHECK(hipFree(c->dy));
+    if (c->scratch)
+        HIPCHECK(hipFree(c->scratch));
+    HIPCHECK(hipEventDestroy(c->ev0));
+    HIPCHECK(hipEventDestroy(c->ev1));
+    HIPCHECK(hipStreamDestroy(c->stream));
+    delete c;
+    R->chain = nullptr;
+}
+
+void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, float *y)
+{
+    ctx *c = get(R, "rt_gemv");
+    check_shape(c, "rt_gemv", w, rows, cols);
+    if (!x || !y)
+        fail("rt_gemv", "x and y must be host arrays");
+    job j = {w, rows, cols, 1, x, y, 0, 0};
+    run_round(c, &j, 1);
+}
+
+void rt_gemv_q(struct rt *R, const void *w, long rows, long cols, const float *x, float *y)
+{
+    ctx *c = get(R, "rt_gemv_q");
+    check_shape(c, "rt_gemv_q", w, rows, cols);
+    if (c->queued >= RT_BATCH)
+        fail("rt_gemv_q", "more than RT_BATCH (8) products queued");
+    c->queue[c->queued++] = job{w, rows, cols, 1, x, y, 0, 0};
+}
+
+void rt_gemm_q(struct rt *R, const void *w, long rows, long cols, const float *x, long t, float *y)
+{
+    ctx *c = get(R, "rt_gemm_q");
+    check_shape(c, "rt_gemm_q", w, rows, cols);
+    if (t < 1)
+        fail("rt_gemm_q", "t must be at least 1");
+    if (c->queued >= RT_BATCH)
+        fail("rt_gemm_q", "more than RT_BATCH (8) products queued");
+    c->queue[c->queued++] = job{w, rows, cols, t, x, y, 0, 0};
+}
+
+void rt_gemv_open(struct rt *R) { (void)get(R, "rt_gemv_open"); }
+
+void rt_gemv_go(struct rt *R)
+{
+    ctx *c = get(R, "rt_gemv_go");
+    if (c->queued)
+        run_round(c, c->queue, c->queued);
+    c->queued = 0;
+}
+
+void rt_gemm(struct rt *R, const void *w, long rows, long cols, const float *x, long t, float *y)
+{
+    ctx *c = get(R, "rt_gemm");
+    check_shape(c, "rt_gemm", w, rows, cols);
+    if (t < 1)
+        fail("rt_gemm", "t must be at least 1");
+    job j = {w, rows, cols, t, x, y, 0, 0};
+    run_round(c, &j, 1);
+}
+
+long gemv_i_bytes(long rows, long cols) { return rows / Q8_GROUP * (cols / Q8_BLOCK) * 544; }
+
+void gemv_i_repack(const uint8_t *q8, long rows, long cols, void *out)
+{
+    if (!q8 || !out || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK)
+        fail("gemv_i_repack", "needs q8, out, rows a positive multiple of 16, cols of 32");
+    const long nb = cols / Q8_BLOCK;
+    uint8_t *o = (uint8_t *)out;
+    for (long g = 0; g < rows / Q8_GROUP; g++) {
+        uint8_t *grp = o + g * 17 * cols;
+        for (int r = 0; r < Q8_GROUP; r++) {
+            const uint8_t *src = q8 + (g * Q8_GROUP + r) * nb * Q8_BLOCK_BYTES;
+            uint8_t *q = grp + r * cols, *d = grp + Q8_GROUP * cols + r * (cols / 16);
+            for (long b = 0; b < nb; b++) {
+                memcpy(q + b * Q8_BLOCK, src + b * Q8_BLOCK_BYTES + 2, Q8_BLOCK);
+                memcpy(d + 2 * b, src + b * Q8_BLOCK_BYTES, 2);
+            }
+        }
+    }
+}
+
+static const void *register_matrix(ctx *c, void *dev, long rows, long cols)
+{
+    c->weights[dev] = matrix{rows, cols};
+    return dev;
+}
+
+const void *rt_q8_upload(struct rt *R, const uint8_t *q8, long rows, long cols)
+{
+    ctx *c = get(R, "rt_q8_upload");
+    if (!q8 || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK)
+        fail("rt_q8_upload", "needs q8, rows a positive multiple of 16, cols of 32");
+    const size_t bytes = (size_t)gemv_i_bytes(rows, cols);
+    void *raw = nullptr, *out = nullptr;
+    if (hipMalloc(&out, bytes) != hipSuccess)
+        return nullptr;
+    if (hipMalloc(&raw, bytes) != hipSuccess) {
+        HIPCHECK(hipFree(out));
+        return nullptr;
+    }
+    HIPCHECK(hipMemcpyAsync(raw, q8, bytes, hipMemcpyHostToDevice, c->stream));
+    q8_launch_repack((q8_stream_t)c->stream, raw, rows, cols, out);
+    launched("the repack");
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    HIPCHECK(hipFree(raw));
+    return register_matrix(c, out, rows, cols);
+}
+
+const void *rt_q8_upload_packed(struct rt *R, const void *packed, long rows, long cols)
+{
+    ctx *c = get(R, "rt_q8_upload_packed");
+    if (!packed || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK)
+        fail("rt_q8_upload_packed", "needs packed, rows a positive multiple of 16, cols of 32");
+    const size_t bytes = (size_t)gemv_i_bytes(rows, cols);
+    void *out = nullptr;
+    if (hipMalloc(&out, bytes) != hipSuccess)
+        return nullptr;
+    HIPCHECK(hipMemcpyAsync(out, packed, bytes, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    return register_matrix(c, out, rows, cols);
+}
+
+void rt_q8_free(struct rt *R, const void *w)
+{
+    ctx *c = get(R, "rt_q8_free");
+    auto it = c->weights.find(w);
+    if (it == c->weights.end())
+        fail("rt_q8_free", "w is not a handle from rt_q8_upload");
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    HIPCHECK(hipFree((void *)w));
+    c->weights.erase(it);
+}
+
+void rt_gemv_dev(struct rt *R, const void *w, long rows, long cols, const float *x, float *y)
+{
+    rt_gemm_dev(R, w, rows, cols, x, cols, 1, y);
+}
+
+void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y)
+{
+    ctx *c = get(R, "rt_gemm_dev");
+    check_shape(c, "rt_gemm_dev", w, rows, cols);
+    check_dev_ptr("rt_gemm_dev", x, "x");
+    check_dev_ptr("rt_gemm_dev", y, "y");
+    if (t < 1 || x_stride < cols || x_stride % 4)
+        fail("rt_gemm_dev", "t >= 1 and x_stride >= cols, a multiple of 4");
+    product(c, w, nullptr, rows, cols, x, x_stride, t, y);
+}
+
+void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y)
+{
+    ctx *c = get(R, "rt_gemv_swiglu_dev");
+    check_shape(c, "rt_gemv_swiglu_dev", wg, rows, cols);
+    check_shape(c, "rt_gemv_swiglu_dev", wu, rows, cols);
+    check_dev_ptr("rt_gemv_swiglu_dev", x, "x");
+    check_dev_ptr("rt_gemv_swiglu_dev", y, "y");
+    if (t < 1 || x_stride < cols || x_stride % 4)
+        fail("rt_gemv_swiglu_dev", "t >= 1 and x_stride >= cols, a multiple of 4");
+    product(c, wg, wu, rows, cols, x, x_stride, t, y);
+}
+
+void *rt_dev_alloc(struct rt *R, long bytes)
+{
+    (void)get(R, "rt_dev_alloc");
+    void *p = nullptr;
+    if (bytes <= 0 || hipMalloc(&p, (size_t)bytes) != hipSuccess)
+        return nullptr;
+    return p;
+}
+
+void rt_dev_free(struct rt *R, void *p)
+{
+    ctx *c = get(R, "rt_dev_free");
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    HIPCHECK(hipFree(p));
+}
+
+void rt_dev_upload(struct rt *R, void *dst, const void *src, long bytes)
+{
+    ctx *c = get(R, "rt_dev_upload");
+    HIPCHECK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, c->stream));
+    HIPCHECK(hipStreamSynchronize(c->stream));
+}
+
+void rt_dev_download(struct rt *R, void *dst, const void *src, long bytes)
+{
+    ctx *c = get(R, "rt_dev_download");
+    HIPCHECK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(hipStreamSynchronize(c->stream));
+}
+
+void rt_dev_sync(struct rt *R) { HIPCHECK(hipStreamSynchronize(get(R, "rt_dev_sync")->stream)); }
+
+void rt_q8_fill_dev(struct rt *R, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma)
+{
+    ctx *c = get(R, "rt_q8_fill_dev");
+    if (!dst || rows <= 0 || cols <= 0 || cols % Q8_BLOCK || ((uintptr_t)dst & 1))
+        fail("rt_q8_fill_dev", "needs an even device address, rows > 0, cols a positive multiple of 32");
+    q8_launch_fill((q8_stream_t)c->stream, dst, rows, cols, seed, dist, mu, sigma);
+    launched("the fill");
+}
+
+void rt_q8_repack_dev(struct rt *R, const void *q8_dev, long rows, long cols, void *out_dev)
+{
+    ctx *c = get(R, "rt_q8_repack_dev");
+    if (!q8_dev || !out_dev || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK || ((uintptr_t)out_dev & 31) || ((uintptr_t)q8_dev & 1))
+        fail("rt_q8_repack_dev", "needs rows a positive multiple of 16, cols of 32, out 32-byte aligned");
+    q8_launch_repack((q8_stream_t)c->stream, q8_dev, rows, cols, out_dev);
+    launched("the repack");
+}
+
+void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed)
+{
+    ctx *c = get(R, "rt_f32_fill_dev");
+    if (!dst || n <= 0)
+        fail("rt_f32_fill_dev", "needs dst and n > 0");
+    q8_launch_fill_f32((q8_stream_t)c->stream, dst, n, seed);
+    launched("the fill");
+}
+
+void rt_prims_dev(struct rt *R, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h, const float *xf,
+                  const float *cf, float *of, long nf)
+{
+    ctx *c = get(R, "rt_prims_dev");
+    if (n8 % 4)
+        fail("rt_prims_dev", "n8 must be a multiple of 4");
+    q8_launch_prims((q8_stream_t)c->stream, q, x8, c8, o8, n8, h, xf, cf, of, nf);
+    launched("the primitive gate");
+}
+
+int rt_set_exact(struct rt *R, int exact)
+{
+    ctx *c = get(R, "rt_set_exact");
+    const int old = c->exact;
+    c->exact = exact != 0;
+    return old;
+}
+
+void rt_timer_start(struct rt *R)
+{
+    ctx *c = get(R, "rt_timer_start");
+    HIPCHECK(hipEventRecord(c->ev0, c->stream));
+}
+
+float rt_timer_stop(struct rt *R)
+{
+    ctx *c = get(R, "rt_timer_stop");
+    float ms = 0.0f;
+    HIPCHECK(hipEventRecord(c->ev1, c->stream));
+    HIPCHECK(hipEventSynchronize(c->ev1));
+    HIPCHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    return ms;
+}
+
+void rt_device_info(struct rt *R, char *name, long name_len, int *cus)
+{
+    ctx *c = get(R, "rt_device_info");
+    hipDeviceProp_t p;
+    HIPCHECK(hipGetDeviceProperties(&p, c->device));
+    if (name && name_len > 0) {
+        snprintf(name, (size_t)name_len, "%s (%s)", p.name, p.gcnArchName);
+    }
+    if (cus)
+        *cus = p.multiProcessorCount;
+}
+
+} /* extern "C" */

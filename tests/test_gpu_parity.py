@@ -1,0 +1,328 @@
+"""GPU parity: the HIP kernels through the C-ABI against the oracle. Every test here needs the MI355X.
+
+  - the primitive conversions reproduce the reference's gate 2.1 lanes;
+  - the GPU repack writes form S byte for byte;
+  - the reference-order kernels are bit-identical to the reference's own products (fixtures made
+    from its compiled sources) and to the oracle at the configurations' shapes;
+  - the fast kernels meet NRMSE <= 1e-5 and max rel <= 1e-4 (tests/parity.py) against the F64
+    closed form, at every configuration's shape and token count, and are deterministic;
+  - the host-pointer entry points (rt_gemv, rt_gemm, the queued round) equal the device ones.
+"""
+import ctypes as c
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import synth
+from parity import assert_parity, metrics
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+class Dev:
+    """Device buffers for one product, freed on exit."""
+
+    def __init__(self, rt):
+        self.rt, self.bufs = rt, []
+
+    def put(self, a):
+        p = self.rt.alloc(max(a.nbytes, 16))
+        self.rt.to_dev(p, a)
+        self.bufs.append(p)
+        return p
+
+    def empty(self, nbytes):
+        p = self.rt.alloc(max(nbytes, 16))
+        self.bufs.append(p)
+        return p
+
+    def get(self, p, shape, dtype):
+        a = np.empty(shape, dtype)
+        self.rt.from_dev(a, p)
+        return a
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *e):
+        for p in self.bufs:
+            self.rt.free(p)
+
+
+def gpu_gemm(rt, q8, rows, cols, x, exact=False, w=None):
+    """Y [t rows] = X W^T through rt_q8_upload + rt_gemm_dev."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    t = x.shape[0]
+    old = rt.set_exact(exact)
+    try:
+        own = w is None
+        if own:
+            w = rt.upload(q8, rows, cols)
+        with Dev(rt) as d:
+            dx, dy = d.put(x), d.empty(4 * t * rows)
+            rt.lib.rt_gemm_dev(rt.R, c.c_void_p(w), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(dy))
+            y = d.get(dy, (t, rows), np.float32)
+        if own:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+    finally:
+        rt.set_exact(old)
+    return y
+
+
+def gpu_swiglu(rt, q8g, q8u, rows, cols, x, exact=False):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    t = x.shape[0]
+    old = rt.set_exact(exact)
+    wg, wu = rt.upload(q8g, rows, cols), rt.upload(q8u, rows, cols)
+    try:
+        with Dev(rt) as d:
+            dx, dy = d.put(x), d.empty(4 * t * rows)
+            rt.lib.rt_gemv_swiglu_dev(rt.R, c.c_void_p(wg), c.c_void_p(wu), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(dy))
+            y = d.get(dy, (t, rows), np.float32)
+    finally:
+        rt.lib.rt_q8_free(rt.R, c.c_void_p(wg))
+        rt.lib.rt_q8_free(rt.R, c.c_void_p(wu))
+        rt.set_exact(old)
+    return y
+
+
+def test_device_is_gfx950(rt):
+    name, cus = rt.device_info()
+    say("device:", name, "CUs:", cus)
+    assert "gfx950" in name
+
+
+def test_primitive_gate21_lanes(rt, oracle):
+    """The int8 and binary16 converts and the fma of the product kernels, on the reference's gate 2.1
+    inputs: the s8 lanes hash to the golden line (gate-2.1.txt:1); the f16 lanes (all 65536 patterns,
+    twice) equal the oracle's bit for bit except NaN payload quieting, and hash to the golden line
+    when no NaN lane differs."""
+    q, h, x8, c8, xf, cf = oracle.gate21_inputs()
+    s8_want, f16_want = oracle.gate21_arrays()
+    with Dev(rt) as d:
+        pq, ph, px8, pc8, pxf, pcf = (d.put(a) for a in (q, h, x8, c8, xf, cf))
+        po8, pof = d.empty(4 * 512), d.empty(4 * 131072)
+        rt.lib.rt_prims_dev(rt.R, c.c_void_p(pq), c.c_void_p(px8), c.c_void_p(pc8), c.c_void_p(po8), 512, c.c_void_p(ph), c.c_void_p(pxf),
+                            c.c_void_p(pcf), c.c_void_p(pof), 131072)
+        s8 = d.get(po8, 512, np.float32)
+        f16 = d.get(pof, 131072, np.float32)
+    golden = {l.split()[0]: l.split()[4] for l in open(os.path.join(GOLDEN, "gate-2.1.txt")) if l.strip()}
+    assert f"{oracle.hash(s8):016x}" == golden["s8"]
+    assert np.array_equal(s8.view(np.uint32), s8_want.view(np.uint32))
+    nan = np.isnan(f16_want)
+    assert np.array_equal(np.isnan(f16), nan)
+    assert np.array_equal(f16[~nan].view(np.uint32), f16_want[~nan].view(np.uint32))
+    quiet_only = np.all((f16[nan].view(np.uint32) ^ f16_want[nan].view(np.uint32)) & ~np.uint32(0x00400000) == 0)
+    say("f16 gate: NaN lanes", int(nan.sum()), "payload kept up to the quiet bit:", bool(quiet_only),
+        "hash", f"{oracle.hash(f16):016x}", "golden", golden["f16"])
+    if np.array_equal(f16.view(np.uint32), f16_want.view(np.uint32)):
+        assert f"{oracle.hash(f16):016x}" == golden["f16"]
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 32), (48, 96), (64, 512), (4096, 4096)])
+def test_repack_on_device(rt, oracle, rows, cols):
+    q8, _ = synth.case(rows * 7 + cols, rows, cols, 1)
+    with Dev(rt) as d:
+        src, dst = d.put(q8), d.empty(q8.nbytes)
+        rt.lib.rt_q8_repack_dev(rt.R, c.c_void_p(src), rows, cols, c.c_void_p(dst))
+        got = d.get(dst, q8.size, np.uint8)
+    assert np.array_equal(got, oracle.repack_s(q8, rows, cols))
+
+
+def fixtures():
+    z = np.load(os.path.join(GOLDEN, "ref_products.npz"))
+    for i in range(int(z["ncases"][0])):
+        seed, rows, cols, t, logn = (int(v) for v in z[f"c{i}_meta"])
+        yield (seed, rows, cols, t), z[f"c{i}_q8"], z[f"c{i}_x"], z[f"c{i}_y"]
+
+
+def test_exact_kernels_equal_reference_fixtures(rt):
+    """The reference-order kernels reproduce the reference's own gemv/gemm outputs bit for bit, and
+    config 1 (4096x4096, seed 0)."""
+    for case, q8, x, y in fixtures():
+        say("fixture", case)
+        got = gpu_gemm(rt, q8, case[1], case[2], x, exact=True)
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32)), case
+    z = np.load(os.path.join(GOLDEN, "ref_products.npz"))
+    q8, x = synth.case(0, 4096, 4096, 1)
+    got = gpu_gemm(rt, q8, 4096, 4096, x, exact=True)[0]
+    assert np.array_equal(got.view(np.uint32), z["cfg1_y"].view(np.uint32))
+
+
+def test_fast_kernels_on_fixtures(rt, oracle):
+    for case, q8, x, y in fixtures():
+        got = gpu_gemm(rt, q8, case[1], case[2], x)
+        m = assert_parity(got, oracle.gemm_f64(q8, case[1], case[2], x), f"fixture {case}")
+        assert_parity(got, y.astype(np.float64), f"fixture {case} vs the reference's F32")
+        say("fast", case, m)
+
+
+# the configurations' matrices: 2B layer (QKV, out, gate/up, down), 9B layer, and config 1
+SHAPES = [(3072, 2048), (2048, 2048), (6144, 2048), (2048, 6144), (6144, 4096), (4096, 4096), (12288, 4096), (4096, 12288)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+@pytest.mark.parametrize("t", [1, 2, 3, 4])
+def test_fast_gemv_shapes(rt, oracle, rows, cols, t):
+    dist = "lognormal" if t > 1 else "normal"
+    q8, x = synth.case(rows + cols + t, rows, cols, t, dist)
+    say("gemv", rows, cols, t, dist)
+    got = gpu_gemm(rt, q8, rows, cols, x)
+    m = assert_parity(got, oracle.gemm_f64(q8, rows, cols, x), f"{rows}x{cols} t={t}")
+    say("  ", m)
+
+
+@pytest.mark.parametrize("t", [5, 8, 16, 17, 40, 64])
+def test_fast_gemm_tokens(rt, oracle, t):
+    rows, cols = 1024, 4096
+    q8, x = synth.case(300 + t, rows, cols, t)
+    say("gemm", rows, cols, t)
+    got = gpu_gemm(rt, q8, rows, cols, x)
+    assert_parity(got, oracle.gemm_f64(q8, rows, cols, x), f"gemm t={t}")
+
+
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (4096, 12288)])
+def test_fast_gemm_prompt_shapes(rt, oracle, rows, cols):
+    """The prompt configuration: M = 16 and 40 on the 9B FFN matrices."""
+    for t in (16, 40):
+        q8, x = synth.case(rows + t, rows, cols, t)
+        say("prompt gemm", rows, cols, t)
+        got = gpu_gemm(rt, q8, rows, cols, x)
+        assert_parity(got, oracle.gemm_f64(q8, rows, cols, x), f"{rows}x{cols} t={t}")
+
+
+@pytest.mark.parametrize("t", [1, 2, 3, 4])
+def test_fused_gate_up(rt, oracle, t):
+    """SiLU(G) * U for the 9B FFN pair (2 x 12288x4096), heavy-tailed scales."""
+    rows, cols = 12288, 4096
+    rng = np.random.default_rng(900 + t)
+    q8g = synth.q8_rows(rng, rows, cols, "lognormal")
+    q8u = synth.q8_rows(rng, rows, cols, "lognormal")
+    x = synth.x_f32(rng, t, cols)
+    say("swiglu", t)
+    got = gpu_swiglu(rt, q8g, q8u, rows, cols, x)
+    want = oracle.swiglu_f64(oracle.gemm_f64(q8g, rows, cols, x), oracle.gemm_f64(q8u, rows, cols, x))
+    m = assert_parity(got, want, f"swiglu t={t}")
+    say("  ", m)
+    ex = gpu_swiglu(rt, q8g, q8u, rows, cols, x, exact=True)
+    assert_parity(ex, want, f"exact swiglu t={t}")
+
+
+def test_exact_kernels_at_config_shapes(rt, oracle):
+    """Bit-identical to the oracle (the reference's order) at the 9B shapes, tokens 1 and 3."""
+    for rows, cols, t in [(4096, 12288, 1), (6144, 4096, 3)]:
+        q8, x = synth.case(rows + 2 * cols + t, rows, cols, t)
+        got = gpu_gemm(rt, q8, rows, cols, x, exact=True)
+        assert np.array_equal(got.view(np.uint32), oracle.gemm(q8, rows, cols, x, threads=8).view(np.uint32))
+
+
+def test_deterministic_and_prefix(rt):
+    """Repeated products give the same bits; the first 1024 rows of a 4096-row handle (the draft
+    head's use, src/apl/qwen35.apl:170-172) give the first 1024 outputs."""
+    rows, cols = 4096, 4096
+    q8, x = synth.case(4242, rows, cols, 2)
+    w = rt.upload(q8, rows, cols)
+    a = gpu_gemm(rt, q8, rows, cols, x, w=w)
+    b = gpu_gemm(rt, q8, rows, cols, x, w=w)
+    p = gpu_gemm(rt, q8, 1024, cols, x, w=w)
+    rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(p.view(np.uint32), a[:, :1024].view(np.uint32))
+
+
+def test_host_pointer_entry_points(rt):
+    """rt_gemv, rt_gemm and a queued round of 4 products sharing x (open/go) give the same bits as the
+    device entry points."""
+    rows, cols = 2048, 2048
+    rng = np.random.default_rng(31)
+    mats = [synth.q8_rows(rng, rows, cols) for _ in range(4)]
+    x = synth.x_f32(rng, 6, cols)
+    ws = [rt.upload(m, rows, cols) for m in mats]
+    try:
+        want1 = [gpu_gemm(rt, m, rows, cols, x[0], w=w)[0] for m, w in zip(mats, ws)]
+        y = np.empty(rows, np.float32)
+        rt.gemv(ws[0], rows, cols, x[0], y)
+        assert np.array_equal(y.view(np.uint32), want1[0].view(np.uint32))
+        ys = [np.empty(rows, np.float32) for _ in range(4)]
+        rt.gemv_open()
+        for w, yy in zip(ws, ys):
+            rt.gemv_q(w, rows, cols, x[0], yy)
+        rt.gemv_go()
+        for yy, wv in zip(ys, want1):
+            assert np.array_equal(yy.view(np.uint32), wv.view(np.uint32))
+        for t in (2, 6):
+            Y = np.empty((t, rows), np.float32)
+            rt.gemm(ws[1], rows, cols, x[:t], t, Y)
+            assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, mats[1], rows, cols, x[:t], w=ws[1]).view(np.uint32))
+        # a mixed round: two gemv sharing x and a gemm
+        Y = np.empty((6, rows), np.float32)
+        rt.gemv_q(ws[2], rows, cols, x[0], ys[0])
+        rt.gemm_q(ws[3], rows, cols, x, 6, Y)
+        rt.gemv_q(ws[0], rows, cols, x[0], ys[1])
+        rt.gemv_go()
+        assert np.array_equal(ys[0].view(np.uint32), want1[2].view(np.uint32))
+        assert np.array_equal(ys[1].view(np.uint32), want1[0].view(np.uint32))
+        assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, mats[3], rows, cols, x, w=ws[3]).view(np.uint32))
+    finally:
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
+def test_edge_scales(rt, oracle):
+    """Zero scales give +0; subnormal, largest-finite and negative binary16 scales; q at -128..127 (the
+    GGUF byte range, wider than the generator's)."""
+    rows, cols = 64, 1024
+    rng = np.random.default_rng(5)
+    q = rng.integers(-128, 128, size=(rows, cols), dtype=np.int8)
+    d = np.zeros((rows, cols // 32), np.float16)
+    d[16:32] = np.float16(6.0e-8)  # the smallest subnormal
+    d[32:48] = rng.integers(1, 1024, size=(16, cols // 32)).astype(np.uint16).view(np.float16)  # every subnormal class
+    d[48:64] = -np.float16(65504.0) / np.float16(1 << 14)
+    q8 = synth.join(q, d)
+    x = synth.x_f32(rng, 2, cols)
+    want = oracle.gemm_f64(q8, rows, cols, x)
+    for exact in (False, True):
+        got = gpu_gemm(rt, q8, rows, cols, x, exact=exact)
+        assert np.all(got[:, :16].view(np.uint32) == 0)
+        assert_parity(got[:, 16:], want[:, 16:], f"edge scales exact={exact}")
+    ex = gpu_gemm(rt, q8, rows, cols, x, exact=True)
+    assert np.array_equal(ex.view(np.uint32), oracle.gemm(q8, rows, cols, x).view(np.uint32))
+
+
+def test_fill_generator(rt):
+    """rt_q8_fill_dev: q in [-127, 127], roughly uniform; d = |N(0, 0.02)|/127 in binary16; the bytes
+    are a function of the seed."""
+    rows, cols = 1024, 4096
+    with Dev(rt) as d:
+        p = d.empty(rows * cols // 32 * 34)
+        rt.lib.rt_q8_fill_dev(rt.R, c.c_void_p(p), rows, cols, 7, 0, 0.0, 0.02)
+        a = d.get(p, rows * cols // 32 * 34, np.uint8)
+        rt.lib.rt_q8_fill_dev(rt.R, c.c_void_p(p), rows, cols, 7, 0, 0.0, 0.02)
+        b = d.get(p, rows * cols // 32 * 34, np.uint8)
+    assert np.array_equal(a, b)
+    q, dd = synth.split(a, rows, cols)
+    assert q.min() == -127 and q.max() == 127
+    assert abs(q.astype(np.float64).mean()) < 0.1
+    df = dd.astype(np.float64)
+    assert np.all(np.isfinite(df)) and np.all(df >= 0)
+    assert abs(df.mean() / (0.02 * np.sqrt(2 / np.pi) / 127) - 1) < 0.01
+
+
+def test_c_drop_in_caller(tmp_path):
+    """tests/c/drop_in.c, a C program written against include/q8_rt.h alone, passes its checks."""
+    exe = tmp_path / "drop_in"
+    lib_dir = os.path.join(ROOT, "intel-phi-apl_amd")
+    subprocess.run(["gcc", "-std=gnu11", "-O2", "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "c", "drop_in.c"), "-L", lib_dir,
+                    "-lq8rt", "-Wl,-rpath," + lib_dir, "-lm", "-o", str(exe)], check=True)
+    p = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    say(p.stdout)
+    assert p.returncode == 0, p.stdout + p.stderr

@@ -1,0 +1,180 @@
+"""The oracle pinned: against the reference's golden gate files, its compiled sources, fixtures made
+from them, exact rational arithmetic and invariants. CPU only."""
+import hashlib
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import synth
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden_lines(name):
+    return [l.split() for l in open(os.path.join(GOLDEN, name)).read().splitlines() if l.strip()]
+
+
+def test_gate_a_fma(oracle):
+    """fmaf's single rounding on the reference's gate A inputs (tests/golden/gate-a.txt:1)."""
+    (line,) = golden_lines("gate-a.txt")
+    h, c0, c1, clast = oracle.gate_a()
+    assert line == ["n", "4096", "hash", f"{h:016x}", "c0", f"{c0:08x}", "c1", f"{c1:08x}", "clast", f"{clast:08x}"]
+
+
+def test_gate21_conversions(oracle):
+    """int8, uint8, binary16 (all 65536 patterns) and the 16-lane tree, the reference's gate 2.1
+    golden hashes (tests/golden/gate-2.1.txt:1-7), in file order."""
+    got = oracle.gate21()
+    want = golden_lines("gate-2.1.txt")
+    assert [w[0] for w in want] == ["s8", "u8fma", "u8mul", "b16", "bcast", "f16", "hsum"]
+    assert [f"{g:016x}" for g in got] == [w[4] for w in want]
+
+
+def test_half_exhaustive(oracle):
+    """binary16 -> binary32 for all 65536 patterns against numpy's conversion (exact): non-NaN bit
+    for bit, NaN to NaN with the same sign and payload (t_knc_half.c:19-40)."""
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32).view(np.uint32)
+    got = np.array([oracle.half(v) for v in range(65536)], np.float32).view(np.uint32)
+    nan = ((h >> 10) & 31 == 31) & (h & 1023 != 0)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.array_equal(got[nan] & ~np.uint32(0x00400000), want[nan] & ~np.uint32(0x00400000))
+
+
+def load_fixtures():
+    z = np.load(os.path.join(GOLDEN, "ref_products.npz"))
+    cases = []
+    for i in range(int(z["ncases"][0])):
+        seed, rows, cols, t, logn = (int(v) for v in z[f"c{i}_meta"])
+        cases.append((seed, rows, cols, t, logn, z[f"c{i}_q8"], z[f"c{i}_x"], z[f"c{i}_y"]))
+    return z, cases
+
+
+def test_fixture_inputs_regenerate():
+    """The fixtures' inputs are what tests/synth.py draws from their seeds (so the GPU tests can use
+    either)."""
+    z, cases = load_fixtures()
+    for seed, rows, cols, t, logn, q8, x, _ in cases:
+        q8b, xb = synth.case(seed, rows, cols, t, "lognormal" if logn else "normal")
+        assert np.array_equal(q8, q8b) and np.array_equal(x, xb)
+    q8, x = synth.case(0, 4096, 4096, 1)
+    assert hashlib.sha256(q8.tobytes()).digest() == z["cfg1_sha_q8"].tobytes()
+    assert hashlib.sha256(x.tobytes()).digest() == z["cfg1_sha_x"].tobytes()
+
+
+def test_oracle_matches_reference_fixtures(oracle):
+    """Bit for bit against the reference's compiled gemv/gemm outputs (tests/golden/ref_products.npz)."""
+    z, cases = load_fixtures()
+    for seed, rows, cols, t, logn, q8, x, y in cases:
+        got = oracle.gemm(q8, rows, cols, x)
+        assert np.array_equal(got.view(np.uint32), y.view(np.uint32)), (seed, rows, cols, t)
+        got_mt = oracle.gemm(q8, rows, cols, x, threads=3)
+        assert np.array_equal(got_mt.view(np.uint32), y.view(np.uint32))
+    q8, x = synth.case(0, 4096, 4096, 1)
+    assert np.array_equal(oracle.gemm(q8, 4096, 4096, x)[0].view(np.uint32), z["cfg1_y"].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols,t", [(16, 512, 1), (16, 512, 2), (64, 512, 3), (512, 512, 4), (1888, 512, 5), (16, 512, 6), (16, 512, 7),
+                                         (64, 512, 8), (16, 512, 9), (16, 512, 15), (512, 512, 16), (16, 512, 17), (64, 512, 40), (32, 4096, 2)])
+def test_oracle_matches_compiled_reference(oracle, reference, rows, cols, t):
+    """Against the reference's gemm_i_thread / gemv_i_thread built from its sources, the shapes of its
+    own gemm == gemv gate (scripts/check.sh:132-149)."""
+    if reference is None:
+        pytest.skip("oracle/_ref not built (the reference's sources are not in this container)")
+    q8, x = synth.case(1000 + rows + t, rows, cols, t)
+    y_ref = reference.gemm(q8, rows, cols, x)
+    assert np.array_equal(oracle.gemm(q8, rows, cols, x).view(np.uint32), y_ref.view(np.uint32))
+    assert np.array_equal(reference.gemv(q8, rows, cols, x[0]).view(np.uint32), y_ref[0].view(np.uint32))
+
+
+def test_f64_closed_form_exact_rationals(oracle):
+    """The F64 closed form against exact rational arithmetic on tiny shapes: every term d*q*x is exact
+    in F64 and the sum of 64 of them differs from the exact sum by at most 64 ulp."""
+    for seed in range(4):
+        rows, cols = 16, 64
+        q8, x = synth.case(50 + seed, rows, cols, 1)
+        q, d = synth.split(q8, rows, cols)
+        got = oracle.gemm_f64(q8, rows, cols, x)[0]
+        for r in range(rows):
+            exact = sum(Fraction(float(d[r, k // 32])) * int(q[r, k]) * Fraction(float(x[0, k])) for k in range(cols))
+            assert abs(Fraction(got[r]) - exact) <= abs(exact) * Fraction(64, 2**53) + Fraction(1, 2**1000)
+
+
+def test_f32_order_close_to_f64(oracle):
+    """The reference's F32 order stays within F32 rounding of the closed form (config 1's shape)."""
+    from parity import metrics
+
+    q8, x = synth.case(0, 4096, 4096, 1)
+    m = metrics(oracle.gemm(q8, 4096, 4096, x), oracle.gemm_f64(q8, 4096, 4096, x))
+    assert m["nrmse"] < 1e-6 and m["max_rel"] < 2e-5, m
+
+
+def test_invariants(oracle):
+    """x = e_j gives column j of d*q exactly; zero scales give +0; permuting 16-row groups permutes y;
+    a prefix of groups is the product of those rows."""
+    rows, cols = 64, 256
+    q8, x = synth.case(77, rows, cols, 1)
+    q, d = synth.split(q8, rows, cols)
+    for j in (0, 31, 32, 255):
+        e = np.zeros(cols, np.float32)
+        e[j] = 1.0
+        col = oracle.gemm(q8, rows, cols, e)[0]
+        assert np.array_equal(col, (d[:, j // 32].astype(np.float32) * q[:, j].astype(np.float32)))
+    z = synth.join(q, np.zeros_like(d))
+    y0 = oracle.gemm(z, rows, cols, x)[0]
+    assert np.all(y0.view(np.uint32) == 0)
+    y = oracle.gemm(q8, rows, cols, x)[0]
+    perm = np.array([2, 0, 3, 1])
+    qp = q.reshape(4, 16, cols)[perm].reshape(rows, cols)
+    dp = d.reshape(4, 16, cols // 32)[perm].reshape(rows, cols // 32)
+    yp = oracle.gemm(synth.join(qp, dp), rows, cols, x)[0]
+    assert np.array_equal(yp, y.reshape(4, 16)[perm].reshape(-1))
+    assert np.array_equal(oracle.gemm(q8[: 32 * cols // 32 * 34], 32, cols, x)[0], y[:32])
+
+
+def test_linearity_f64(oracle):
+    rows, cols = 32, 512
+    q8, x = synth.case(5, rows, cols, 2)
+    a, b = 0.75, -2.5
+    xc = (a * x[0].astype(np.float64) + b * x[1].astype(np.float64)).astype(np.float32)
+    y = oracle.gemm_f64(q8, rows, cols, x)
+    yc = oracle.gemm_f64(q8, rows, cols, xc)[0]
+    # xc is rounded to F32: compare with the F64 product of the rounded input's linear parts
+    assert np.allclose(yc, a * y[0] + b * y[1], rtol=1e-6, atol=1e-6 * np.abs(y).max())
+
+
+def test_repack_s_definition(oracle):
+    """Form S byte by byte against an independent index formula."""
+    rows, cols = 48, 96
+    q8, _ = synth.case(9, rows, cols, 1)
+    q, d = synth.split(q8, rows, cols)
+    got = oracle.repack_s(q8, rows, cols)
+    want = np.concatenate([np.concatenate([q[16 * g:16 * g + 16].view(np.uint8).ravel(), d[16 * g:16 * g + 16].view(np.uint8).ravel()])
+                           for g in range(rows // 16)])
+    assert np.array_equal(got, want)
+
+
+def test_planted_mistakes_are_caught(oracle):
+    """The checks have teeth: plausible slips in an F32 product (one term dropped, the scale of a
+    neighbouring block, a transposed operand, a sign) each fail the parity bar against the F64 form."""
+    from parity import metrics
+
+    rows, cols = 64, 512
+    q8, x = synth.case(21, rows, cols, 1)
+    q, d = synth.split(q8, rows, cols)
+    ref = oracle.gemm_f64(q8, rows, cols, x)[0]
+    qf, df, xf = q.astype(np.float64), np.repeat(d.astype(np.float64), 32, axis=1), x[0].astype(np.float64)
+
+    def fails(y):
+        m = metrics(y, ref)
+        return m["nrmse"] > 1e-5 or m["max_rel"] > 1e-4
+
+    assert not fails((qf * df) @ xf)
+    dropped = qf.copy()
+    dropped[:, 100] = 0
+    assert fails((dropped * df) @ xf)
+    assert fails((qf * np.roll(df, 32, axis=1)) @ xf)
+    assert fails((qf * df)[:, ::-1] @ xf)
+    assert fails((-qf * df) @ xf)
