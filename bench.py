@@ -1,0 +1,389 @@
+#!/usr/bin/env python3
+"""Benchmark of the Q8_0 weight products on one MI355X.
+
+The step is one 9B-class decode token at M = 1: 32 layers of
+    QKV 6144x4096, out 4096x4096, gate+up 2 x 12288x4096 fused into SiLU(g)*u, down 4096x12288,
+then the output head 151936x4096: 129 products, 7,230,391,808 B of Q8_0 weights resident in HBM
+(distinct per layer, synthetic: q uniform in [-127, 127], d = binary16(|N(0, 0.02)|/127)), every
+byte streamed once per token. Activations are already in HBM. The token is recorded once as a
+HIP graph and replayed.
+
+value = algorithmic bytes per token (Q8_0 weights + x read once + y written once, per product)
+        x tokens / time, in GB/s; ms_per_step = ms per token.
+roofline = the dominant kernel (the fused gate+up): its algorithmic bytes per launch over its
+        average duration, from events attached to each of its launches in a timed replay.
+cpu_baseline = the reference's own host path (oracle/_ref: src/card/gemv.c with the team of
+        src/card/team.c, built from the reference's sources) on this host's cores, over one 9B
+        layer's five products; the oracle's own restatement when oracle/_ref is absent.
+
+Also in the line, each measured with its own weights rotated through >= 512 MB so that the
+256 MB Infinity Cache cannot serve them: the single 4096x4096 GEMV, the draft head (first 32768
+rows), the prompt GEMM at M = 16 and 40, the verify path at M = 2..4 (fused pair + down,
+heavy-tailed scales), and the 2B layer set.
+"""
+import argparse
+import ctypes as c
+import importlib.util
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
+MALL_ROTATE_BYTES = 512 << 20
+
+HIDDEN, FFN, QKV, VOCAB, DRAFT, LAYERS = 4096, 12288, 4096 + 2 * 1024, 151936, 32768, 32
+
+
+def package():
+    spec = importlib.util.spec_from_file_location("q8rt", os.path.join(ROOT, "intel-phi-apl_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["q8rt"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def q8_bytes(rows, cols):
+    return rows * cols // 32 * 34
+
+
+def alg_bytes(rows, cols, t, pair=False):
+    """Weights once, x once, y once (the fused pair: both weights, x once, SiLU(g)*u once)."""
+    return q8_bytes(rows, cols) * (2 if pair else 1) + 4 * t * cols + 4 * t * rows
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self, q8rt):
+        self.q8rt = q8rt
+        self.rt = q8rt.Runtime()
+        self.lib, self.R = self.rt.lib, self.rt.R
+        self.staging = self.rt.alloc(q8_bytes(VOCAB, HIDDEN))
+        self.seed = 1000
+
+    def matrix(self, rows, cols, dist=0, mu=0.0, sigma=0.02):
+        """Synthetic GGUF rows drawn on the GPU, repacked to the device form: a resident handle."""
+        self.seed += 1
+        w = self.rt.alloc(q8_bytes(rows, cols))
+        self.lib.rt_q8_fill_dev(self.R, c.c_void_p(self.staging), rows, cols, self.seed, dist, mu, sigma)
+        self.lib.rt_q8_repack_dev(self.R, c.c_void_p(self.staging), rows, cols, c.c_void_p(w))
+        return w
+
+    def vec(self, n):
+        self.seed += 1
+        p = self.rt.alloc(4 * n)
+        self.lib.rt_f32_fill_dev(self.R, c.c_void_p(p), n, self.seed)
+        return p
+
+    def gemm(self, w, rows, cols, x, t, y, xs=None):
+        self.lib.rt_gemm_dev(self.R, c.c_void_p(w), rows, cols, c.c_void_p(x), xs or cols, t, c.c_void_p(y))
+
+    def pair(self, wg, wu, rows, cols, x, t, y):
+        self.lib.rt_gemv_swiglu_dev(self.R, c.c_void_p(wg), c.c_void_p(wu), rows, cols, c.c_void_p(x), cols, t, c.c_void_p(y))
+
+    def timed(self, fn, reps):
+        self.rt.sync()
+        self.lib.rt_timer_start(self.R)
+        for _ in range(reps):
+            fn()
+        return self.lib.rt_timer_stop(self.R) / reps
+
+    def ktimes(self, fn, reps):
+        """Per-launch kernel durations (us) of every product fn makes, by (kind, rows, cols, t)."""
+        self.lib.rt_ktime(self.R, 1)
+        for _ in range(reps):
+            fn()
+        n = 16384
+        kind, rows, cols, t = (np.zeros(n, np.int32), np.zeros(n, np.int64), np.zeros(n, np.int64), np.zeros(n, np.int64))
+        us = np.zeros(n, np.float32)
+        got = self.lib.rt_ktime_read(self.R, *(self.q8rt.ptr(a) for a in (kind, rows, cols, t, us)), n)
+        self.lib.rt_ktime(self.R, 0)
+        out = {}
+        for i in range(got):
+            out.setdefault((self.q8rt.KINDS[int(kind[i])], int(rows[i]), int(cols[i]), int(t[i])), []).append(float(us[i]))
+        return out
+
+
+def rotation(bench, rows, cols, copies_min=2, **kw):
+    per = q8_bytes(rows, cols)
+    n = max(copies_min, -(-MALL_ROTATE_BYTES // per))
+    return [bench.matrix(rows, cols, **kw) for _ in range(n)]
+
+
+def decode_9b(b, steps, warmup):
+    log(f"9B decode: {LAYERS} layers + head, {7230391808 / 1e9:.2f} GB of Q8_0 weights")
+    layers = [dict(qkv=b.matrix(QKV, HIDDEN), out=b.matrix(HIDDEN, HIDDEN), gate=b.matrix(FFN, HIDDEN), up=b.matrix(FFN, HIDDEN),
+                   down=b.matrix(HIDDEN, FFN)) for _ in range(LAYERS)]
+    head = b.matrix(VOCAB, HIDDEN)
+    xh, xa, h = b.vec(HIDDEN), b.vec(HIDDEN), b.vec(FFN)
+    yq, yo, yd, logits = b.vec(QKV), b.vec(HIDDEN), b.vec(HIDDEN), b.vec(VOCAB)
+
+    def token():
+        for L in layers:
+            b.gemm(L["qkv"], QKV, HIDDEN, xh, 1, yq)
+            b.gemm(L["out"], HIDDEN, HIDDEN, xa, 1, yo)
+            b.pair(L["gate"], L["up"], FFN, HIDDEN, xh, 1, h)
+            b.gemm(L["down"], HIDDEN, FFN, h, 1, yd)
+        b.gemm(head, VOCAB, HIDDEN, xh, 1, logits)
+
+    per_token = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) +
+                          alg_bytes(HIDDEN, FFN, 1)) + alg_bytes(VOCAB, HIDDEN, 1)
+    b.lib.rt_graph_begin(b.R)
+    token()
+    graph = b.lib.rt_graph_end(b.R)
+    run = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(graph))  # noqa: E731
+    for _ in range(warmup):
+        run()
+    ms_graph = b.timed(run, steps)
+    ms_eager = b.timed(token, max(1, steps // 4))
+    log(f"  token: graph {ms_graph:.3f} ms, eager {ms_eager:.3f} ms")
+    kt = b.ktimes(token, min(steps, 100))
+    b.lib.rt_graph_free(b.R, c.c_void_p(graph))
+    kernels = {}
+    for (kind, rows, cols, t), v in sorted(kt.items()):
+        pair = kind.endswith("pair")
+        mean = statistics.fmean(v)
+        gbs = alg_bytes(rows, cols, t, pair) / mean / 1e3
+        kernels[f"{kind} {rows}x{cols} t{t}"] = {"us": round(mean, 3), "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                                                 "launches": len(v)}
+        log(f"  {kind:9s} {rows:6d}x{cols:<5d} t{t}: {mean:8.2f} us  {gbs:7.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
+    # the dominant kernel: the most time per token
+    dom = max(kt.items(), key=lambda kv: statistics.fmean(kv[1]) * len(kv[1]))
+    (kind, rows, cols, t), v = dom
+    per_launch = alg_bytes(rows, cols, t, kind.endswith("pair"))
+    mean_us = statistics.fmean(v)
+    roof = {"kernel": f"gemv_s<1,4,{1 if kind.endswith('pair') else 0}> ({kind} {rows}x{cols}, t={t})", "bound": "hbm",
+            "achieved": round(per_launch / mean_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(per_launch / mean_us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": per_launch,
+            "us_per_launch": round(mean_us, 3), "launches_timed": len(v)}
+    return per_token, ms_graph, ms_eager, kernels, roof, layers
+
+
+def single_gemv(b):
+    """Config 1's shape on the GPU: 4096x4096, rotated through >= 512 MB of copies."""
+    ws = rotation(b, 4096, 4096)
+    x, y = b.vec(4096), b.vec(4096)
+    kt = b.ktimes(lambda: [b.gemm(w, 4096, 4096, x, 1, y) for w in ws], 4)
+    us = statistics.fmean(next(iter(kt.values())))
+    ms = b.timed(lambda: [b.gemm(w, 4096, 4096, x, 1, y) for w in ws], 4) / len(ws)
+    for w in ws:
+        b.rt.free(w)
+    gb = alg_bytes(4096, 4096, 1)
+    return {"kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "back_to_back_us": round(1e3 * ms, 3), "copies": len(ws)}
+
+
+def draft_head(b):
+    ws = rotation(b, DRAFT, HIDDEN)
+    x, y = b.vec(HIDDEN), b.vec(DRAFT)
+    kt = b.ktimes(lambda: [b.gemm(w, DRAFT, HIDDEN, x, 1, y) for w in ws], 4)
+    us = statistics.fmean(next(iter(kt.values())))
+    for w in ws:
+        b.rt.free(w)
+    gb = alg_bytes(DRAFT, HIDDEN, 1)
+    return {"rows": DRAFT, "kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "copies": len(ws)}
+
+
+def prompt_gemm(b):
+    """Config 4: Y = X W^T, M = 16 and 40, on gate/up 12288x4096 and down 4096x12288."""
+    out = {}
+    for rows, cols in ((FFN, HIDDEN), (HIDDEN, FFN)):
+        ws = rotation(b, rows, cols)
+        x, y = b.vec(40 * cols), b.vec(40 * rows)
+        for m in (16, 40):
+            kt = b.ktimes(lambda: [b.gemm(w, rows, cols, x, m, y) for w in ws], 3)
+            us = statistics.fmean([u for v in kt.values() for u in v])
+            flop = 2.0 * m * rows * cols
+            out[f"M{m} {rows}x{cols}"] = {"kernel_us": round(us, 3), "GFLOPS": round(flop / us / 1e3, 1),
+                                          "GB/s": round(alg_bytes(rows, cols, m) / us / 1e3, 1), "kernel": sorted({k[0] for k in kt})}
+        for w in ws:
+            b.rt.free(w)
+        b.rt.free(x)
+        b.rt.free(y)
+    return out
+
+
+def verify_path(b):
+    """Config 5: M = 2..4 tokens, fused gate+up (2 x 12288x4096) then down 4096x12288, d lognormal(ln 0.002, 1)."""
+    kw = dict(dist=1, mu=float(np.log(0.002)), sigma=1.0)
+    per = 2 * q8_bytes(FFN, HIDDEN) + q8_bytes(HIDDEN, FFN)
+    n = max(2, -(-MALL_ROTATE_BYTES // per))
+    sets = [(b.matrix(FFN, HIDDEN, **kw), b.matrix(FFN, HIDDEN, **kw), b.matrix(HIDDEN, FFN, **kw)) for _ in range(n)]
+    x, h, y = b.vec(4 * HIDDEN), b.vec(4 * FFN), b.vec(4 * HIDDEN)
+    out = {}
+    for m in (2, 3, 4):
+        def step():
+            for g, u, d in sets:
+                b.pair(g, u, FFN, HIDDEN, x, m, h)
+                b.gemm(d, HIDDEN, FFN, h, m, y)
+        kt = b.ktimes(step, 3)
+        res = {}
+        for (kind, rows, cols, t), v in kt.items():
+            pair = kind.endswith("pair")
+            us = statistics.fmean(v)
+            res["fused_gate_up" if pair else "down"] = {"kernel_us": round(us, 3), "GB/s": round(alg_bytes(rows, cols, t, pair) / us / 1e3, 1)}
+        out[f"M{m}"] = res
+    for s in sets:
+        for w in s:
+            b.rt.free(w)
+    return out
+
+
+def layers_2b(b):
+    """Config 2: 24 layers of QKV 3072x2048, out 2048x2048, gate/up 6144x2048 (fused), down 2048x6144."""
+    H, F, Q = 2048, 6144, 2048 + 2 * 512
+    layers = [(b.matrix(Q, H), b.matrix(H, H), b.matrix(F, H), b.matrix(F, H), b.matrix(H, F)) for _ in range(24)]
+    xh, h, yq, yo, yd = b.vec(H), b.vec(F), b.vec(Q), b.vec(H), b.vec(H)
+
+    def run():
+        for qkv, o, g, u, d in layers:
+            b.gemm(qkv, Q, H, xh, 1, yq)
+            b.gemm(o, H, H, xh, 1, yo)
+            b.pair(g, u, F, H, xh, 1, h)
+            b.gemm(d, H, F, h, 1, yd)
+
+    per = 24 * (alg_bytes(Q, H, 1) + alg_bytes(H, H, 1) + alg_bytes(F, H, 1, pair=True) + alg_bytes(H, F, 1))
+    b.lib.rt_graph_begin(b.R)
+    run()
+    g = b.lib.rt_graph_end(b.R)
+    b.lib.rt_graph_launch(b.R, c.c_void_p(g))
+    ms = b.timed(lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(g)), 20)
+    b.lib.rt_graph_free(b.R, c.c_void_p(g))
+    for L in layers:
+        for w in L:
+            b.rt.free(w)
+    return {"us_per_pass": round(1e3 * ms, 2), "GB/s": round(per / ms / 1e6, 1), "bytes": per}
+
+
+def cpu_baseline(b, layer, seconds):
+    """The reference's host path on this host's cores over one 9B layer's products (bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    threads = min(16, len(os.sched_getaffinity(0)))
+    shapes = [("qkv", QKV, HIDDEN), ("out", HIDDEN, HIDDEN), ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN)]
+    # the layer's GGUF rows, drawn again on the GPU from their seeds and copied to the host
+    mats = []
+    seed0 = layer["seed0"]
+    for i, (name, rows, cols) in enumerate(shapes):
+        b.lib.rt_q8_fill_dev(b.R, c.c_void_p(b.staging), rows, cols, seed0 + i, 0, 0.0, 0.02)
+        raw = np.empty(q8_bytes(rows, cols), np.uint8)
+        b.rt.from_dev(raw, b.staging)
+        mats.append((rows, cols, raw))
+    rng = np.random.default_rng(0)
+    xs = {cols: rng.standard_normal(cols, dtype=np.float32) for _, _, cols in shapes}
+    nbytes = sum(alg_bytes(r, k, 1) for _, r, k in shapes)
+    try:
+        from oracle_ffi import Reference
+
+        ref = Reference()
+        kind = "reference"
+        forms = []
+        for rows, cols, raw in mats:
+            fi = ref.repack_i(raw, rows, cols)
+            forms.append((rows, cols, fi, np.empty(rows, np.float32)))
+        team = ref.lib.ref_team_create(threads)
+        if not team:
+            raise OSError("team")
+
+        def one():
+            for rows, cols, fi, y in forms:
+                ref.lib.ref_team_gemv_i(c.c_void_p(team), c.c_void_p(fi.ctypes.data), rows, cols, c.c_void_p(xs[cols].ctypes.data),
+                                        c.c_void_p(y.ctypes.data))
+        done = lambda: ref.lib.ref_team_destroy(c.c_void_p(team))  # noqa: E731
+    except (FileNotFoundError, OSError):
+        from oracle_ffi import Oracle
+
+        orc = Oracle()
+        kind = "port"
+        outs = [np.empty(r, np.float32) for r, _, _ in mats]
+
+        def one():
+            for (rows, cols, raw), y in zip(mats, outs):
+                orc.lib.q8o_gemm_mt(c.c_void_p(raw.ctypes.data), rows, cols, c.c_void_p(xs[cols].ctypes.data), cols, 1, c.c_void_p(y.ctypes.data), threads)
+        done = lambda: None  # noqa: E731
+    one()  # warm-up, dropped (src/bench/gemv_bench.c:113-125)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    done()
+    med = statistics.median(times)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"one 9B decode layer (QKV 6144x4096, out 4096x4096, gate and up 12288x4096, down 4096x12288: {nbytes} B), "
+                      f"median of {len(times)} passes after one warm-up, {threads} threads pinned to this host's CPUs",
+            "ms_per_layer": round(1e3 * med, 2), "host_cpus": os.cpu_count()}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (every product runs on one MI355X; see DESIGN.md "
+              "for how the rows would shard across GPUs)", file=sys.stderr)
+        sys.exit(2)
+    q8rt = package()
+    b = Bench(q8rt)
+    name, cus = b.rt.device_info()
+    log(f"device: {name}, {cus} CUs")
+    seed0 = b.seed + 1
+    per_token, ms_graph, ms_eager, kernels, roof, layers = decode_9b(b, a.steps, a.warmup)
+    layer0 = {"seed0": seed0}
+    extra = {}
+    if not a.no_extra:
+        for key, fn in (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
+                        ("2b_layer_set", layers_2b)):
+            log(f"{key} ...")
+            extra[key] = fn(b)
+            log(f"  {json.dumps(extra[key])}")
+    cpu = None
+    if not a.no_cpu:
+        log("CPU baseline ...")
+        cpu = cpu_baseline(b, layer0, a.cpu_seconds)
+        log(f"  {json.dumps(cpu)}")
+    value = per_token / ms_graph / 1e6
+    gm = extra.get("prompt_gemm", {}).get(f"M16 {FFN}x{HIDDEN}")
+    line = {
+        "metric": "Q8_0 GEMV HBM GB/s (% of peak) at 9B decode; M=16 GEMM GFLOPS",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_graph, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (Q8_0 int8 weights, binary16 scales)",
+        "data": "synthetic (seeded on the GPU: q uniform in [-127,127], d = binary16(|N(0,0.02)|/127), x ~ N(0,1))",
+        "config": {"workload": "9B-class decode token, M=1: 32 x (QKV 6144x4096, out 4096x4096, gate+up 2x12288x4096 fused SiLU(g)*u, "
+                               "down 4096x12288) + head 151936x4096; one HIP graph per token",
+                   "bytes_per_token": per_token, "products_per_token": 4 * LAYERS + 1},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "eager_ms_per_step": round(ms_eager, 4),
+        "gemm_m16_gflops": gm["GFLOPS"] if gm else None,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "device": name,
+        "kernels_9b": kernels,
+        "configs": extra,
+    }
+    print(json.dumps(line), flush=True)
+    b.rt.close()
+
+
+if __name__ == "__main__":
+    main()

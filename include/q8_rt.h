@@ -126,6 +126,15 @@ void rt_dev_upload(struct rt *R, void *dst, const void *src, long bytes);
 void rt_dev_download(struct rt *R, void *dst, const void *src, long bytes);
 void rt_dev_sync(struct rt *R);
 
+/* A recorded sequence of device products, replayed with one call (a HIP graph captured from
+ * the runtime's stream): rt_graph_begin, then any rt_*_dev products (no host-pointer products,
+ * no copies), then rt_graph_end returns the sequence; rt_graph_launch enqueues one replay on the
+ * stream, in order with every other product. The pointers recorded are used as they are. */
+void rt_graph_begin(struct rt *R);
+void *rt_graph_end(struct rt *R);
+void rt_graph_launch(struct rt *R, void *graph);
+void rt_graph_free(struct rt *R, void *graph);
+
 /* ---- host-side tests and benchmarks (additions) */
 
 /* Synthetic GGUF Q8_0 rows written on the GPU at dst (device, rows*cols/32*34 bytes): q uniform
@@ -153,6 +162,18 @@ int rt_set_exact(struct rt *R, int exact);
  * milliseconds between them (waits for the stream). */
 void rt_timer_start(struct rt *R);
 float rt_timer_stop(struct rt *R);
+
+/* Kernel timing, for the benchmark: while on, every product records its (first) kernel's own
+ * start and end (events attached to the kernel's dispatch), up to 16384 products; rt_ktime_read
+ * waits for the stream and returns how many it filled: the kind (RT_K_*), the shape and the
+ * kernel's duration in microseconds; reading clears the records. rt_ktime(R, 1) also clears. */
+#define RT_K_GEMV 0      /* t <= 4, the decode kernel */
+#define RT_K_GEMV_PAIR 1 /* the fused gate/up pair, t <= 4 */
+#define RT_K_GEMM 2      /* t >= 5, the matrix-core kernel */
+#define RT_K_GEMM_PAIR 3
+#define RT_K_EXACT 4 /* the reference-order kernel */
+void rt_ktime(struct rt *R, int on);
+long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, long max);
 
 /* The device's name and its count of compute units, for reports. */
 void rt_device_info(struct rt *R, char *name, long name_len, int *cus);

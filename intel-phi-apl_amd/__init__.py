@@ -58,7 +58,15 @@ _SIGS = {
     "rt_timer_start": (None, [_vp]),
     "rt_timer_stop": (_c.c_float, [_vp]),
     "rt_device_info": (None, [_vp, _c.c_char_p, _long, _c.POINTER(_int)]),
+    "rt_graph_begin": (None, [_vp]),
+    "rt_graph_end": (_vp, [_vp]),
+    "rt_graph_launch": (None, [_vp, _vp]),
+    "rt_graph_free": (None, [_vp, _vp]),
+    "rt_ktime": (None, [_vp, _int]),
+    "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _long]),
 }
+
+KINDS = {0: "gemv", 1: "gemv_pair", 2: "gemm", 3: "gemm_pair", 4: "exact"}
 
 
 def header_symbols(path=HEADER):

@@ -54,6 +54,24 @@ __device__ __forceinline__ float q8_wave_sum(float v)
     return v;
 }
 
+#define Q8_DPP(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xf, 0xf, false))
+
+/* sum over the 64 lanes by DPP within each row of 16 lanes (pairs i^1, i^2, then the half-row
+ * and row mirrors), then the four rows' sums read from lanes 15, 31, 47, 63 and added as
+ * (r0 + r1) + (r2 + r3): the same order on every call; the result is wave-uniform */
+__device__ __forceinline__ float q8_wave_sum_dpp(float v)
+{
+    v += Q8_DPP(v, 0xb1);  /* quad_perm [1,0,3,2] */
+    v += Q8_DPP(v, 0x4e);  /* quad_perm [2,3,0,1] */
+    v += Q8_DPP(v, 0x141); /* row_half_mirror */
+    v += Q8_DPP(v, 0x140); /* row_mirror */
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 15));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 47));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    return (r0 + r1) + (r2 + r3);
+}
+
 /* SiLU(g) * u (src/apl/qwen35.apl:38; docs/model.md:29: Sig = 1 / (1 + exp(min(700, -g)))):
  * in binary32 exp(min(700, -g)) overflows to inf for -g > 88.7 exactly as exp(-g) does, so
  * the clamp changes nothing and is left out. */
@@ -67,6 +85,26 @@ __device__ __forceinline__ float q8_swiglu(float g, float u)
 #ifdef __cplusplus
 struct ihipStream_t;
 typedef struct ihipStream_t *q8_stream_t;
+
+/* Kernel timing: when set, the next product kernel launched takes these two events as its own
+ * start and end (hipExtLaunchKernelGGL), then the slot clears. Host side, one thread. */
+void q8_time_next(void *start_event, void *stop_event);
+
+#if defined(__HIPCC__)
+#include <hip/hip_ext.h>
+extern void *q8_next_start, *q8_next_stop;
+/* kernel<<<grid, block, 0, stream>>>(args...), or the timed launch when a slot is set */
+#define Q8_LAUNCH(kernel, grid, block, stream, ...)                                                                    \
+    do {                                                                                                               \
+        if (q8_next_start) {                                                                                           \
+            hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (hipEvent_t)q8_next_start, (hipEvent_t)q8_next_stop, 0, \
+                                  __VA_ARGS__);                                                                        \
+            q8_next_start = q8_next_stop = nullptr;                                                                    \
+        } else {                                                                                                       \
+            kernel<<<grid, block, 0, stream>>>(__VA_ARGS__);                                                           \
+        }                                                                                                              \
+    } while (0)
+#endif
 
 /* Y = X W^T, t tokens, the fast kernels; W form S. w1 != NULL: the fused pair, Y = SiLU(X W0^T) * (X W1^T). */
 void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);

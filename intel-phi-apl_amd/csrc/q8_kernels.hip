@@ -20,6 +20,14 @@
 
 /* ---------------------------------------------------------------- decode GEMV */
 
+void *q8_next_start = nullptr, *q8_next_stop = nullptr;
+
+void q8_time_next(void *start_event, void *stop_event)
+{
+    q8_next_start = start_event;
+    q8_next_stop = stop_event;
+}
+
 #define GEMV_WAVES 4 /* waves per workgroup */
 
 template <int MT, int RW, int PAIR>
@@ -106,12 +114,121 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_s(const uint8_t *__restr
     }
 }
 
+/* The decode kernel for cols % 1024 == 0: a workgroup of NW waves owns RW rows (one group's
+ * quarter) and all of K; wave w takes the K-slice [w*1024*S, (w+1)*1024*S), S steps of 64
+ * 16-column units. Every load of a lane (P*RW*S weight units and their scales, then x) is
+ * issued before any arithmetic, so the whole matrix is in flight in the first round trip: the
+ * small layer matrices are latency-bound otherwise. Then per lane the same arithmetic as
+ * gemv_s; the lanes' partials summed by q8_wave_sum_dpp, the waves' in LDS in wave order. */
+template <int MT, int RW, int S, int PAIR>
+__global__ __launch_bounds__(256) void gemv_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
+                                              const float *__restrict__ x, long x_stride, float *__restrict__ y)
+{
+    constexpr int P = PAIR + 1;
+    __shared__ float red[4][P * RW * MT];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const long r0 = (long)blockIdx.x * RW;
+    const long u0 = (long)wave * 64 * S + lane;
+
+    uint4 q[P][RW][S];
+    uint16_t dh[P][RW][S];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const uint8_t *w = p ? w1 : w0;
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const uint8_t *wq = w + q8s_row_q(r0 + r, cols);
+            const uint16_t *wd = (const uint16_t *)(w + q8s_row_d(r0 + r, cols));
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                q[p][r][s] = *(const uint4 *)(wq + 16 * (u0 + 64 * s));
+                dh[p][r][s] = wd[(u0 + 64 * s) >> 1];
+            }
+        }
+    }
+    float4 xv[MT][S][4];
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+        for (int s = 0; s < S; s++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                xv[m][s][c] = *(const float4 *)(x + m * x_stride + 16 * (u0 + 64 * s) + 4 * c);
+
+    float acc[P][RW][MT];
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                acc[p][r][m] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+                const uint32_t qw[4] = {q[p][r][s].x, q[p][r][s].y, q[p][r][s].z, q[p][r][s].w};
+                float wf[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    wf[j] = q8_s8(qw[j >> 2], j & 3);
+                const float d = q8_half(dh[p][r][s]);
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    const float xs[16] = {xv[m][s][0].x, xv[m][s][0].y, xv[m][s][0].z, xv[m][s][0].w, xv[m][s][1].x, xv[m][s][1].y,
+                                          xv[m][s][1].z, xv[m][s][1].w, xv[m][s][2].x, xv[m][s][2].y, xv[m][s][2].z, xv[m][s][2].w,
+                                          xv[m][s][3].x, xv[m][s][3].y, xv[m][s][3].z, xv[m][s][3].w};
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 16; j++)
+                        sum = __builtin_fmaf(wf[j], xs[j], sum);
+                    acc[p][r][m] = __builtin_fmaf(sum, d, acc[p][r][m]);
+                }
+            }
+#pragma unroll
+    for (int p = 0; p < P; p++)
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const float v = q8_wave_sum_dpp(acc[p][r][m]);
+                if (lane == 0)
+                    red[wave][(p * RW + r) * MT + m] = v;
+            }
+    __syncthreads();
+    if (threadIdx.x < RW * MT) {
+        const int r = threadIdx.x / MT, m = threadIdx.x % MT;
+        float v[P];
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            v[p] = red[0][(p * RW + r) * MT + m];
+            for (int w = 1; w < nw; w++)
+                v[p] += red[w][(p * RW + r) * MT + m];
+        }
+        y[m * rows + r0 + r] = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
+    }
+}
+
 template <int MT, int RW, int PAIR>
 static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y)
 {
+    const long kb = cols / 1024;
+    const int nw = cols % 1024 ? 0 : kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
+    const long steps = nw ? kb / nw : 0;
+    const dim3 grid((unsigned)(rows / RW)), block(64 * nw);
+    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
+    switch (steps) {
+    case 1: Q8_LAUNCH((gemv_k<MT, RW, 1, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 2: Q8_LAUNCH((gemv_k<MT, RW, 2, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 3: Q8_LAUNCH((gemv_k<MT, RW, 3, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 4: Q8_LAUNCH((gemv_k<MT, RW, 4, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    default: break;
+    }
+    /* any other cols (a multiple of 32): the loop over K */
     const long waves = rows / RW;
-    const dim3 grid((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES));
-    gemv_s<MT, RW, PAIR><<<grid, 64 * GEMV_WAVES, 0, s>>>((const uint8_t *)w0, (const uint8_t *)w1, rows, cols, x, xs, y);
+    Q8_LAUNCH((gemv_s<MT, RW, PAIR>), dim3((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), s, a, b, rows, cols, x, xs, y);
 }
 
 template <int RW, int PAIR>
@@ -168,7 +285,7 @@ __global__ __launch_bounds__(256) void exact_s(const uint8_t *__restrict__ w, lo
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y)
 {
     const long n = rows * t;
-    exact_s<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)w, rows, cols, x, x_stride, t, y);
+    Q8_LAUNCH(exact_s, dim3((unsigned)((n + 255) / 256)), dim3(256), (hipStream_t)stream, (const uint8_t *)w, rows, cols, x, x_stride, t, y);
 }
 
 __global__ __launch_bounds__(256) void swiglu_ew(const float *__restrict__ g, const float *__restrict__ u, long n, float *__restrict__ y)

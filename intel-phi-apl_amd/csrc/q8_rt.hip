@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/q8_rt.h"
 #include "q8_device.h"
@@ -37,6 +38,11 @@ struct matrix {
     long rows, cols;
 };
 
+struct ktrec {
+    int kind;
+    long rows, cols, t;
+};
+
 struct job {
     const void *w;
     long rows, cols, t;
@@ -59,7 +65,13 @@ struct ctx {
     std::unordered_map<const void *, matrix> weights;
     job queue[RT_BATCH];
     int queued = 0;
+    /* kernel timing (rt_ktime): one event pair per recorded product */
+    int ktime_on = 0;
+    std::vector<hipEvent_t> kt_events;
+    std::vector<ktrec> kt;
 };
+
+constexpr size_t KT_MAX = 16384;
 
 ctx *get(struct rt *R, const char *fn)
 {
@@ -144,6 +156,12 @@ void launched(const char *what)
 void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y)
 {
     q8_stream_t s = (q8_stream_t)c->stream;
+    if (c->ktime_on && c->kt.size() < KT_MAX) {
+        const size_t i = c->kt.size();
+        const int kind = c->exact ? RT_K_EXACT : (t <= 4 ? RT_K_GEMV : RT_K_GEMM) + (w1 ? 1 : 0);
+        q8_time_next(c->kt_events[2 * i], c->kt_events[2 * i + 1]);
+        c->kt.push_back(ktrec{kind, rows, cols, t});
+    }
     if (c->exact) {
         if (!w1) {
             q8_launch_exact(s, w0, rows, cols, x, xs, t, y);
@@ -255,6 +273,8 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipFree(c->dy));
     if (c->scratch)
         HIPCHECK(hipFree(c->scratch));
+    for (auto &e : c->kt_events)
+        HIPCHECK(hipEventDestroy(e));
     HIPCHECK(hipEventDestroy(c->ev0));
     HIPCHECK(hipEventDestroy(c->ev1));
     HIPCHECK(hipStreamDestroy(c->stream));
@@ -504,6 +524,68 @@ float rt_timer_stop(struct rt *R)
     HIPCHECK(hipEventSynchronize(c->ev1));
     HIPCHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
     return ms;
+}
+
+void rt_graph_begin(struct rt *R)
+{
+    ctx *c = get(R, "rt_graph_begin");
+    if (c->ktime_on)
+        fail("rt_graph_begin", "kernel timing is on: switch it off before recording");
+    HIPCHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+}
+
+void *rt_graph_end(struct rt *R)
+{
+    ctx *c = get(R, "rt_graph_end");
+    hipGraph_t g = nullptr;
+    hipGraphExec_t e = nullptr;
+    HIPCHECK(hipStreamEndCapture(c->stream, &g));
+    HIPCHECK(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
+    HIPCHECK(hipGraphDestroy(g));
+    return (void *)e;
+}
+
+void rt_graph_launch(struct rt *R, void *graph)
+{
+    ctx *c = get(R, "rt_graph_launch");
+    HIPCHECK(hipGraphLaunch((hipGraphExec_t)graph, c->stream));
+}
+
+void rt_graph_free(struct rt *R, void *graph)
+{
+    ctx *c = get(R, "rt_graph_free");
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    HIPCHECK(hipGraphExecDestroy((hipGraphExec_t)graph));
+}
+
+void rt_ktime(struct rt *R, int on)
+{
+    ctx *c = get(R, "rt_ktime");
+    if (on && c->kt_events.empty()) {
+        c->kt_events.resize(2 * KT_MAX);
+        for (auto &e : c->kt_events)
+            HIPCHECK(hipEventCreate(&e));
+    }
+    c->kt.clear();
+    c->ktime_on = on != 0;
+}
+
+long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, long max)
+{
+    ctx *c = get(R, "rt_ktime_read");
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    const long n = (long)c->kt.size() < max ? (long)c->kt.size() : max;
+    for (long i = 0; i < n; i++) {
+        float ms = 0.0f;
+        HIPCHECK(hipEventElapsedTime(&ms, c->kt_events[2 * i], c->kt_events[2 * i + 1]));
+        kind[i] = c->kt[i].kind;
+        rows[i] = c->kt[i].rows;
+        cols[i] = c->kt[i].cols;
+        t[i] = c->kt[i].t;
+        us[i] = 1000.0f * ms;
+    }
+    c->kt.clear();
+    return n;
 }
 
 void rt_device_info(struct rt *R, char *name, long name_len, int *cus)
