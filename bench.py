@@ -68,6 +68,7 @@ class Bench:
         self.lib, self.R = self.rt.lib, self.rt.R
         self.staging = self.rt.alloc(q8_bytes(VOCAB, HIDDEN))
         self.seed = 1000
+        self.knames = {}
 
     def matrix(self, rows, cols, dist=0, mu=0.0, sigma=0.02):
         """Synthetic GGUF rows drawn on the GPU, repacked to the device form: a resident handle."""
@@ -97,18 +98,22 @@ class Bench:
         return self.lib.rt_timer_stop(self.R) / reps
 
     def ktimes(self, fn, reps):
-        """Per-launch kernel durations (us) of every product fn makes, by (kind, rows, cols, t)."""
+        """Per-launch kernel durations (us) of every product fn makes, by (kind, rows, cols, t); the
+        kernel's name and grid (threads) as rocprof reports them in self.knames[(kind, rows, cols, t)]."""
         self.lib.rt_ktime(self.R, 1)
         for _ in range(reps):
             fn()
         n = 16384
         kind, rows, cols, t = (np.zeros(n, np.int32), np.zeros(n, np.int64), np.zeros(n, np.int64), np.zeros(n, np.int64))
-        us = np.zeros(n, np.float32)
-        got = self.lib.rt_ktime_read(self.R, *(self.q8rt.ptr(a) for a in (kind, rows, cols, t, us)), n)
+        us, grid = np.zeros(n, np.float32), np.zeros(n, np.int64)
+        names = c.create_string_buffer(64 * n)
+        got = self.lib.rt_ktime_read(self.R, *(self.q8rt.ptr(a) for a in (kind, rows, cols, t, us)), names, self.q8rt.ptr(grid), n)
         self.lib.rt_ktime(self.R, 0)
         out = {}
         for i in range(got):
-            out.setdefault((self.q8rt.KINDS[int(kind[i])], int(rows[i]), int(cols[i]), int(t[i])), []).append(float(us[i]))
+            key = (self.q8rt.KINDS[int(kind[i])], int(rows[i]), int(cols[i]), int(t[i]))
+            out.setdefault(key, []).append(float(us[i]))
+            self.knames[key] = (names.raw[64 * i:64 * i + 64].split(b"\0")[0].decode(), int(grid[i]))
         return out
 
 
@@ -152,17 +157,21 @@ def decode_9b(b, steps, warmup):
         pair = kind.endswith("pair")
         mean = statistics.fmean(v)
         gbs = alg_bytes(rows, cols, t, pair) / mean / 1e3
+        kname, grid = b.knames[(kind, rows, cols, t)]
         kernels[f"{kind} {rows}x{cols} t{t}"] = {"us": round(mean, 3), "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
-                                                 "launches": len(v)}
+                                                 "launches": len(v), "kernel": kname, "grid": grid, "alg_bytes": alg_bytes(rows, cols, t, pair)}
         log(f"  {kind:9s} {rows:6d}x{cols:<5d} t{t}: {mean:8.2f} us  {gbs:7.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
     # the dominant kernel: the most time per token
     dom = max(kt.items(), key=lambda kv: statistics.fmean(kv[1]) * len(kv[1]))
     (kind, rows, cols, t), v = dom
     per_launch = alg_bytes(rows, cols, t, kind.endswith("pair"))
     mean_us = statistics.fmean(v)
-    roof = {"kernel": f"gemv_s<1,4,{1 if kind.endswith('pair') else 0}> ({kind} {rows}x{cols}, t={t})", "bound": "hbm",
+    kname, grid = b.knames[(kind, rows, cols, t)]
+    roof = {"kernel": f"{kname} ({kind} {rows}x{cols}, t={t}, grid {grid})", "bound": "hbm",
             "achieved": round(per_launch / mean_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(per_launch / mean_us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": per_launch,
+            "frac": round(per_launch / mean_us / 1e3 / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(kname, grid),
+            "traffic_source": os.path.relpath(DECODE_PROFILE, ROOT) + " (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by the copy kernel)",
+            "bytes_per_launch": per_launch,
             "us_per_launch": round(mean_us, 3), "launches_timed": len(v)}
     return per_token, ms_graph, ms_eager, kernels, roof, layers
 
@@ -322,6 +331,111 @@ def cpu_baseline(b, layer, seconds):
             "ms_per_layer": round(1e3 * med, 2), "host_cpus": os.cpu_count()}
 
 
+CALIB_BYTES = 1 << 30
+PROFILES = os.path.join(ROOT, "profiles")
+DECODE_PROFILE = os.path.join(PROFILES, "gemv_decode_9b_m1.md")
+PROFILE_CMDS = [
+    "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_stats -o run -- python3 bench.py --steps 20 --warmup 3 "
+    "--no-cpu --no-extra --calib > gpurun_out/prof_stats.log 2>&1",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o run -- python3 bench.py --steps 2 --warmup 1 --no-cpu "
+    "--no-extra --calib",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o run -- python3 bench.py --steps 2 --warmup 1 --no-cpu "
+    "--no-extra --calib",
+    "python3 bench.py --summarize gpurun_out",
+]
+
+
+def _kname(full):
+    """rocprof's kernel name without the return type and the argument list."""
+    n = full.split("(")[0].strip()
+    return n[5:] if n.startswith("void ") else n
+
+
+def summarize(run_dir, out=DECODE_PROFILE):
+    """profiles/gemv_decode_9b_m1.md from the three rocprofv3 runs of PROFILE_CMDS: per product of the
+    token, the kernel, its average duration in the kernel trace and in the benchmark's own events,
+    and its HBM bytes per launch from FETCH_SIZE and WRITE_SIZE, each scaled by what the counter
+    reads for the plain copy kernel over CALIB_BYTES."""
+    import csv
+    from collections import defaultdict
+
+    line = next(json.loads(l) for l in open(os.path.join(run_dir, "prof_stats.log")) if l.startswith('{"metric"'))
+    trace = defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(run_dir, "prof_stats", "run_kernel_trace.csv"))):
+        g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        trace[(_kname(r["Kernel_Name"]), g)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    counters = {}
+    for cname, sub in (("FETCH_SIZE", "prof_fetch"), ("WRITE_SIZE", "prof_write")):
+        acc = defaultdict(list)
+        for r in csv.DictReader(open(os.path.join(run_dir, sub, "run_counter_collection.csv"))):
+            if r["Counter_Name"] == cname:
+                acc[(_kname(r["Kernel_Name"]), int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+        counters[cname] = {k: statistics.fmean(v) for k, v in acc.items()}
+    ck = ("copy16", CALIB_BYTES // 16)
+    scale = {n: CALIB_BYTES / (counters[n][ck] * 1024.0) for n in counters}
+    stats = list(csv.DictReader(open(os.path.join(run_dir, "prof_stats", "run_kernel_stats.csv"))))
+    rows, traffic = [], {}
+    for shape, k in line["kernels_9b"].items():
+        key = (k["kernel"], k["grid"])
+        tr = trace.get(key, [])
+        f, w = counters["FETCH_SIZE"].get(key), counters["WRITE_SIZE"].get(key)
+        tb = None if f is None or w is None else round(1024.0 * (f * scale["FETCH_SIZE"] + w * scale["WRITE_SIZE"]))
+        traffic[f"{k['kernel']} grid {k['grid']}"] = {"shape": shape, "traffic": tb, "alg_bytes": k["alg_bytes"],
+                                                       "trace_us": round(statistics.fmean(tr), 3) if tr else None}
+        rows.append(f"| {shape} | `{k['kernel']}` | {k['grid']} | {len(tr)} | {statistics.fmean(tr) if tr else float('nan'):.2f} | {k['us']:.2f} | "
+                    f"{f if f is not None else float('nan'):.1f} | {w if w is not None else float('nan'):.1f} | {tb} | {k['alg_bytes']} | "
+                    f"{(tb / k['alg_bytes']) if tb else float('nan'):.4f} |")
+    roof = line["roofline"]
+    text = [f"# Decode GEMV kernels, 9B-class token at M = 1 (rocprofv3)", "",
+            f"Device: {line['device']}. Workload: {line['config']['workload']}.", "",
+            "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + PROFILE_CMDS + ["```", "",
+            f"Token under the kernel trace: {line['ms_per_step']} ms with the graph, {line['eager_ms_per_step']} ms eager (the trace "
+            "slows graph replays; the unprofiled figures are the benchmark's).", "",
+            "## Kernel statistics (kernel trace, all launches of the run)", "",
+            "| Kernel | Calls | Average ns | Min ns | Max ns | % of time |", "|---|---|---|---|---|---|"]
+    for r in stats:
+        text.append(f"| `{_kname(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']):.1f} | {r['MinNs']} | {r['MaxNs']} | {r['Percentage']} |")
+    text += ["", "## Per product of the token", "",
+             f"Counter yardstick: the copy kernel over {CALIB_BYTES} B reads FETCH_SIZE "
+             f"{counters['FETCH_SIZE'][ck]:.1f} KiB and WRITE_SIZE {counters['WRITE_SIZE'][ck]:.1f} KiB per launch, so "
+             f"FETCH_SIZE is scaled by {scale['FETCH_SIZE']:.4f} and WRITE_SIZE by {scale['WRITE_SIZE']:.4f}.", "",
+             "| Product | Kernel | Grid (threads) | Launches traced | Trace avg us | Bench event avg us (under the trace) | FETCH_SIZE KiB | WRITE_SIZE KiB | "
+             "HBM bytes (scaled) | Algorithmic bytes | HBM / algorithmic |", "|---|---|---|---|---|---|---|---|---|---|---|"] + rows
+    dk = roof["kernel"].split(" (")[0] + " grid " + roof["kernel"].rsplit("grid ", 1)[1].rstrip(")")
+    dt = traffic.get(dk, {})
+    if dt.get("trace_us"):
+        text += ["", f"Dominant kernel: {roof['kernel']}: {dt['trace_us']} us per launch in the kernel trace, so "
+                 f"{roof['bytes_per_launch'] / dt['trace_us'] / 1e3:.1f} GB/s algorithmic = "
+                 f"{100 * roof['bytes_per_launch'] / dt['trace_us'] / 1e3 / HBM_PEAK_GBS:.1f} % of {HBM_PEAK_GBS:.0f} GB/s (the unprofiled "
+                 "benchmark's events time the same launches)."]
+    text += ["",
+             "Machine-readable (read by bench.py for roofline.traffic):", "", "```json", json.dumps(traffic), "```", ""]
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    open(out, "w").write("\n".join(text))
+    print(f"wrote {out}")
+
+
+def profiled_traffic(kname, grid, path=DECODE_PROFILE):
+    """HBM bytes per launch of (kernel, grid) from the committed rocprofv3 summary, or None."""
+    try:
+        text = open(path).read()
+        blob = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(blob).get(f"{kname} grid {grid}", {}).get("traffic")
+    except (OSError, IndexError, ValueError):
+        return None
+
+
+def calib_copy(b):
+    """Three copies of 1 GiB (4x the Infinity Cache) by the plain copy kernel: each reads and writes
+    every byte once, so a --pmc run's FETCH_SIZE and WRITE_SIZE for it are the counters' yardstick."""
+    src, dst = b.rt.alloc(CALIB_BYTES), b.rt.alloc(CALIB_BYTES)
+    b.lib.rt_f32_fill_dev(b.R, c.c_void_p(src), CALIB_BYTES // 4, 99)
+    ms = b.timed(lambda: b.lib.rt_dev_copy(b.R, c.c_void_p(dst), c.c_void_p(src), CALIB_BYTES), 3)
+    log(f"calibration copy: {CALIB_BYTES} B read + written, {ms:.3f} ms, {2 * CALIB_BYTES / ms / 1e6:.1f} GB/s")
+    b.rt.free(src)
+    b.rt.free(dst)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -330,7 +444,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
+                    "profile commands) and exit")
+    ap.add_argument("--calib", action="store_true", help="also copy 1 GiB three times with the plain copy kernel (the yardstick "
+                    "for the HBM byte counters of a rocprofv3 --pmc run)")
     a = ap.parse_args()
+    if a.summarize:
+        summarize(a.summarize)
+        return
     if a.gpus != 1:
         print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (every product runs on one MI355X; see DESIGN.md "
               "for how the rows would shard across GPUs)", file=sys.stderr)
@@ -339,6 +460,8 @@ def main():
     b = Bench(q8rt)
     name, cus = b.rt.device_info()
     log(f"device: {name}, {cus} CUs")
+    if a.calib:
+        calib_copy(b)
     seed0 = b.seed + 1
     per_token, ms_graph, ms_eager, kernels, roof, layers = decode_9b(b, a.steps, a.warmup)
     layer0 = {"seed0": seed0}

@@ -145,6 +145,9 @@ void rt_q8_fill_dev(struct rt *R, void *dst, long rows, long cols, uint64_t seed
 void rt_q8_repack_dev(struct rt *R, const void *q8_dev, long rows, long cols, void *out_dev);
 /* F32 N(0,1) values on the GPU: a function of (seed, index) only. */
 void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed);
+/* dst = src on the runtime's stream by a plain kernel that reads and writes every byte once
+ * (16-byte aligned, bytes % 16 == 0): the yardstick the benchmark scales the HBM byte counters by. */
+void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes);
 
 /* The product kernels' primitive conversions on the GPU, lane by lane: o8[i] = fma(x8[i],
  * (float)q[i], c8[i]) with the int8 convert of the weights (n8 % 4 == 0), of[i] = fma(xf[i],
@@ -165,15 +168,17 @@ float rt_timer_stop(struct rt *R);
 
 /* Kernel timing, for the benchmark: while on, every product records its (first) kernel's own
  * start and end (events attached to the kernel's dispatch), up to 16384 products; rt_ktime_read
- * waits for the stream and returns how many it filled: the kind (RT_K_*), the shape and the
- * kernel's duration in microseconds; reading clears the records. rt_ktime(R, 1) also clears. */
+ * waits for the stream and returns how many it filled: the kind (RT_K_*), the shape, the kernel's
+ * duration in microseconds, its name as rocprof prints it (64 bytes each in names, NUL-padded;
+ * names may be NULL) and its grid in threads (grid may be NULL); reading clears the records.
+ * rt_ktime(R, 1) also clears. */
 #define RT_K_GEMV 0      /* t <= 4, the decode kernel */
 #define RT_K_GEMV_PAIR 1 /* the fused gate/up pair, t <= 4 */
 #define RT_K_GEMM 2      /* t >= 5, the matrix-core kernel */
 #define RT_K_GEMM_PAIR 3
 #define RT_K_EXACT 4 /* the reference-order kernel */
 void rt_ktime(struct rt *R, int on);
-long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, long max);
+long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, char *names, long *grid, long max);
 
 /* The device's name and its count of compute units, for reports. */
 void rt_device_info(struct rt *R, char *name, long name_len, int *cus);

@@ -53,6 +53,7 @@ _SIGS = {
     "rt_q8_fill_dev": (None, [_vp, _vp, _long, _long, _u64, _int, _c.c_float, _c.c_float]),
     "rt_q8_repack_dev": (None, [_vp, _vp, _long, _long, _vp]),
     "rt_f32_fill_dev": (None, [_vp, _vp, _long, _u64]),
+    "rt_dev_copy": (None, [_vp, _vp, _vp, _long]),
     "rt_prims_dev": (None, [_vp, _vp, _vp, _vp, _vp, _long, _vp, _vp, _vp, _vp, _long]),
     "rt_set_exact": (_int, [_vp, _int]),
     "rt_timer_start": (None, [_vp]),
@@ -63,7 +64,7 @@ _SIGS = {
     "rt_graph_launch": (None, [_vp, _vp]),
     "rt_graph_free": (None, [_vp, _vp]),
     "rt_ktime": (None, [_vp, _int]),
-    "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _long]),
+    "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _long]),
 }
 
 KINDS = {0: "gemv", 1: "gemv_pair", 2: "gemm", 3: "gemm_pair", 4: "exact"}

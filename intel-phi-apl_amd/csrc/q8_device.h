@@ -87,16 +87,24 @@ struct ihipStream_t;
 typedef struct ihipStream_t *q8_stream_t;
 
 /* Kernel timing: when set, the next product kernel launched takes these two events as its own
- * start and end (hipExtLaunchKernelGGL), then the slot clears. Host side, one thread. */
-void q8_time_next(void *start_event, void *stop_event);
+ * start and end (hipExtLaunchKernelGGL) and writes its name, as rocprof prints it (for example
+ * "gemv_k<1, 4, 1, 1>"), into name[64] and its grid in threads into *grid; then the slot
+ * clears. Host side, one thread. */
+void q8_time_next(void *start_event, void *stop_event, char *name, long *grid);
+/* "base<a, b, ...>" for the n integers that follow, into the timing slot's name */
+void q8_time_name(const char *base, int n, ...);
 
 #if defined(__HIPCC__)
 #include <hip/hip_ext.h>
 extern void *q8_next_start, *q8_next_stop;
-/* kernel<<<grid, block, 0, stream>>>(args...), or the timed launch when a slot is set */
-#define Q8_LAUNCH(kernel, grid, block, stream, ...)                                                                    \
+extern long *q8_next_grid;
+/* kernel<<<grid, block, 0, stream>>>(args...), or the timed launch when a slot is set; NAME is
+ * evaluated only then (a call of q8_time_name) */
+#define Q8_LAUNCH(NAME, kernel, grid, block, stream, ...)                                                              \
     do {                                                                                                               \
         if (q8_next_start) {                                                                                           \
+            NAME;                                                                                                      \
+            *q8_next_grid = (long)(grid).x * (grid).y * (grid).z * (block).x * (block).y * (block).z;                 \
             hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (hipEvent_t)q8_next_start, (hipEvent_t)q8_next_stop, 0, \
                                   __VA_ARGS__);                                                                        \
             q8_next_start = q8_next_stop = nullptr;                                                                    \
@@ -119,6 +127,8 @@ void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, 
 /* Synthetic GGUF rows and F32 values on the device. */
 void q8_launch_fill(q8_stream_t stream, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma);
 void q8_launch_fill_f32(q8_stream_t stream, float *dst, long n, uint64_t seed);
+/* dst = src, n16 16-byte words, both device. */
+void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16);
 /* The primitive conversions of the product kernels, lane by lane (the reference's gate 2.1
  * s8 and f16 sets, src/gate/upconv_kernel.c:18-57). */
 void q8_launch_prims(q8_stream_t stream, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h,

@@ -16,16 +16,35 @@
  *   prims       the conversions above, lane by lane, for the known-answer gates. */
 #include <hip/hip_runtime.h>
 
+#include <stdarg.h>
+#include <stdio.h>
+
 #include "q8_device.h"
 
 /* ---------------------------------------------------------------- decode GEMV */
 
 void *q8_next_start = nullptr, *q8_next_stop = nullptr;
+long *q8_next_grid = nullptr;
+static char *q8_next_name = nullptr;
 
-void q8_time_next(void *start_event, void *stop_event)
+void q8_time_next(void *start_event, void *stop_event, char *name, long *grid)
 {
     q8_next_start = start_event;
     q8_next_stop = stop_event;
+    q8_next_name = name;
+    q8_next_grid = grid;
+}
+
+void q8_time_name(const char *base, int n, ...)
+{
+    va_list ap;
+    va_start(ap, n);
+    int k = snprintf(q8_next_name, 64, "%s", base);
+    for (int i = 0; i < n && k < 63; i++)
+        k += snprintf(q8_next_name + k, (size_t)(64 - k), "%s%d", i ? ", " : "<", va_arg(ap, int));
+    if (n && k < 63)
+        snprintf(q8_next_name + k, (size_t)(64 - k), ">");
+    va_end(ap);
 }
 
 #define GEMV_WAVES 4 /* waves per workgroup */
@@ -220,15 +239,15 @@ static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, lo
     const dim3 grid((unsigned)(rows / RW)), block(64 * nw);
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
     switch (steps) {
-    case 1: Q8_LAUNCH((gemv_k<MT, RW, 1, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    case 2: Q8_LAUNCH((gemv_k<MT, RW, 2, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    case 3: Q8_LAUNCH((gemv_k<MT, RW, 3, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    case 4: Q8_LAUNCH((gemv_k<MT, RW, 4, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 1: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 1, PAIR), (gemv_k<MT, RW, 1, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 2: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 2, PAIR), (gemv_k<MT, RW, 2, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 3: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 3, PAIR), (gemv_k<MT, RW, 3, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
+    case 4: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 4, PAIR), (gemv_k<MT, RW, 4, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
     default: break;
     }
     /* any other cols (a multiple of 32): the loop over K */
     const long waves = rows / RW;
-    Q8_LAUNCH((gemv_s<MT, RW, PAIR>), dim3((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), s, a, b, rows, cols, x, xs, y);
+    Q8_LAUNCH(q8_time_name("gemv_s", 3, MT, RW, PAIR), (gemv_s<MT, RW, PAIR>), dim3((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), s, a, b, rows, cols, x, xs, y);
 }
 
 template <int RW, int PAIR>
@@ -285,7 +304,7 @@ __global__ __launch_bounds__(256) void exact_s(const uint8_t *__restrict__ w, lo
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y)
 {
     const long n = rows * t;
-    Q8_LAUNCH(exact_s, dim3((unsigned)((n + 255) / 256)), dim3(256), (hipStream_t)stream, (const uint8_t *)w, rows, cols, x, x_stride, t, y);
+    Q8_LAUNCH(q8_time_name("exact_s", 0), exact_s, dim3((unsigned)((n + 255) / 256)), dim3(256), (hipStream_t)stream, (const uint8_t *)w, rows, cols, x, x_stride, t, y);
 }
 
 __global__ __launch_bounds__(256) void swiglu_ew(const float *__restrict__ g, const float *__restrict__ u, long n, float *__restrict__ y)
@@ -398,6 +417,20 @@ __global__ __launch_bounds__(256) void fill_f32(float *__restrict__ dst, long n,
 void q8_launch_fill_f32(q8_stream_t stream, float *dst, long n, uint64_t seed)
 {
     fill_f32<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>(dst, n, seed);
+}
+
+/* dst = src, n16 16-byte words, one per thread: every byte read once and written once, which
+ * makes it the yardstick for the HBM byte counters. */
+__global__ __launch_bounds__(256) void copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, long n16)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16)
+        dst[i] = src[i];
+}
+
+void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16)
+{
+    copy16<<<dim3((unsigned)((n16 + 255) / 256)), 256, 0, (hipStream_t)stream>>>((uint4 *)dst, (const uint4 *)src, n16);
 }
 
 /* ---------------------------------------------------------------- primitive gates */

@@ -40,7 +40,8 @@ struct matrix {
 
 struct ktrec {
     int kind;
-    long rows, cols, t;
+    long rows, cols, t, grid;
+    char name[64];
 };
 
 struct job {
@@ -159,8 +160,8 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
     if (c->ktime_on && c->kt.size() < KT_MAX) {
         const size_t i = c->kt.size();
         const int kind = c->exact ? RT_K_EXACT : (t <= 4 ? RT_K_GEMV : RT_K_GEMM) + (w1 ? 1 : 0);
-        q8_time_next(c->kt_events[2 * i], c->kt_events[2 * i + 1]);
-        c->kt.push_back(ktrec{kind, rows, cols, t});
+        c->kt.push_back(ktrec{kind, rows, cols, t, 0, {0}});
+        q8_time_next(c->kt_events[2 * i], c->kt_events[2 * i + 1], c->kt.back().name, &c->kt.back().grid);
     }
     if (c->exact) {
         if (!w1) {
@@ -492,6 +493,15 @@ void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed)
     launched("the fill");
 }
 
+void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes)
+{
+    ctx *c = get(R, "rt_dev_copy");
+    if (!dst || !src || bytes <= 0 || bytes % 16 || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15))
+        fail("rt_dev_copy", "needs 16-byte aligned device addresses and bytes a positive multiple of 16");
+    q8_launch_copy((q8_stream_t)c->stream, dst, src, bytes / 16);
+    launched("the copy");
+}
+
 void rt_prims_dev(struct rt *R, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h, const float *xf,
                   const float *cf, float *of, long nf)
 {
@@ -563,6 +573,7 @@ void rt_ktime(struct rt *R, int on)
     ctx *c = get(R, "rt_ktime");
     if (on && c->kt_events.empty()) {
         c->kt_events.resize(2 * KT_MAX);
+        c->kt.reserve(KT_MAX); /* the timing slot points into the last record: no reallocation */
         for (auto &e : c->kt_events)
             HIPCHECK(hipEventCreate(&e));
     }
@@ -570,7 +581,7 @@ void rt_ktime(struct rt *R, int on)
     c->ktime_on = on != 0;
 }
 
-long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, long max)
+long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, char *names, long *grid, long max)
 {
     ctx *c = get(R, "rt_ktime_read");
     HIPCHECK(hipStreamSynchronize(c->stream));
@@ -583,6 +594,10 @@ long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, flo
         cols[i] = c->kt[i].cols;
         t[i] = c->kt[i].t;
         us[i] = 1000.0f * ms;
+        if (names)
+            memcpy(names + 64 * i, c->kt[i].name, 64);
+        if (grid)
+            grid[i] = c->kt[i].grid;
     }
     c->kt.clear();
     return n;
