@@ -249,7 +249,8 @@ int rt_init(struct rt *R, int threads)
     }
     const char *ex = getenv("Q8_EXACT");
     c->exact = ex && atoi(ex) != 0;
-    R->team = nullptr;
+    /* R->team and R->frame belong to the caller, which creates its team before rt_init
+     * (src/card/engine.c:249-250) and keeps using it for the primitives that are not products */
     R->gemm_chain = nullptr;
     R->chain = c;
     R->threads = threads;
