@@ -201,17 +201,29 @@ def draft_head(b):
 
 
 def prompt_gemm(b):
-    """Config 4: Y = X W^T, M = 16 and 40, on gate/up 12288x4096 and down 4096x12288."""
+    """Config 4: Y = X W^T, M = 16 and 40 (and 64), on gate/up 12288x4096 and down 4096x12288.
+
+    kernel_us: the matrix-core kernel alone (events on its launch); product_us: the whole product
+    (the x limb pass and the kernel) back to back over the rotated copies, stream events. GFLOPS
+    counts 2*M*rows*cols; mfma_util is the bf16 MFMA work actually issued (three limbs, tokens
+    padded to 16) over the kernel's time, against the dense bf16 peak."""
     out = {}
     for rows, cols in ((FFN, HIDDEN), (HIDDEN, FFN)):
         ws = rotation(b, rows, cols)
-        x, y = b.vec(40 * cols), b.vec(40 * rows)
-        for m in (16, 40):
+        x, y = b.vec(64 * cols), b.vec(64 * rows)
+        for m in (16, 40, 64):
+            b.gemm(ws[0], rows, cols, x, m, y)  # workspace sized before timing
             kt = b.ktimes(lambda: [b.gemm(w, rows, cols, x, m, y) for w in ws], 3)
             us = statistics.fmean([u for v in kt.values() for u in v])
+            ms = b.timed(lambda: [b.gemm(w, rows, cols, x, m, y) for w in ws], 3) / len(ws)
             flop = 2.0 * m * rows * cols
-            out[f"M{m} {rows}x{cols}"] = {"kernel_us": round(us, 3), "GFLOPS": round(flop / us / 1e3, 1),
-                                          "GB/s": round(alg_bytes(rows, cols, m) / us / 1e3, 1), "kernel": sorted({k[0] for k in kt})}
+            issued = 2.0 * 3 * (16 * -(-m // 16)) * rows * cols
+            kname, grid = b.knames[next(iter(kt))]
+            out[f"M{m} {rows}x{cols}"] = {"kernel": kname, "grid": grid, "kernel_us": round(us, 3), "product_us": round(1e3 * ms, 3),
+                                          "GFLOPS": round(flop / us / 1e3, 1), "GFLOPS_product": round(flop / ms / 1e6, 1),
+                                          "GB/s": round(alg_bytes(rows, cols, m) / us / 1e3, 1),
+                                          "pct_hbm": round(100 * alg_bytes(rows, cols, m) / us / 1e3 / HBM_PEAK_GBS, 1),
+                                          "mfma_util": round(issued / us / 1e6 / BF16_PEAK_TFLOPS, 4), "copies": len(ws)}
         for w in ws:
             b.rt.free(w)
         b.rt.free(x)
@@ -444,6 +456,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", metavar="SECTIONS", help="comma-separated sections to run instead of the full line (gemv_4096x4096, "
+                    "draft_head, prompt_gemm, verify, 2b_layer_set); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
     ap.add_argument("--calib", action="store_true", help="also copy 1 GiB three times with the plain copy kernel (the yardstick "
@@ -460,6 +474,15 @@ def main():
     b = Bench(q8rt)
     name, cus = b.rt.device_info()
     log(f"device: {name}, {cus} CUs")
+    sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
+                ("2b_layer_set", layers_2b))
+    if a.only:
+        want = a.only.split(",")
+        for key, fn in sections:
+            if key in want:
+                print(json.dumps({key: fn(b)}), flush=True)
+        b.rt.close()
+        return
     if a.calib:
         calib_copy(b)
     seed0 = b.seed + 1
@@ -467,8 +490,7 @@ def main():
     layer0 = {"seed0": seed0}
     extra = {}
     if not a.no_extra:
-        for key, fn in (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
-                        ("2b_layer_set", layers_2b)):
+        for key, fn in sections:
             log(f"{key} ...")
             extra[key] = fn(b)
             log(f"  {json.dumps(extra[key])}")
@@ -498,6 +520,7 @@ def main():
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "eager_ms_per_step": round(ms_eager, 4),
         "gemm_m16_gflops": gm["GFLOPS"] if gm else None,
+        "gemm_m16_mfma_util": gm["mfma_util"] if gm else None,
         "roofline": roof,
         "cpu_baseline": cpu,
         "device": name,

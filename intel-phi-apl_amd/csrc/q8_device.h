@@ -118,8 +118,18 @@ extern long *q8_next_grid;
 void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* The reference's order, every y bit-identical to the reference's F32 host path. */
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
-/* Y = X W^T for 5 <= t <= 64 on the matrix cores. */
-void q8_launch_gemm(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* Y = X W^T for 5 <= t <= 64 on the matrix cores: the x limb pass, then the product. xs holds
+ * q8_gemm_xs_bytes(cols, t) bytes, part q8_gemm_part_floats(rows, cols, t) floats (at most
+ * Q8_GEMM_PART_MAX), counters Q8_GEMM_COUNTERS words that are zero, and are zero again after. */
+#define Q8_GEMM_PART_MAX (8L << 20)
+#define Q8_GEMM_COUNTERS 1024
+void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, void *xs, float *part,
+                         uint32_t *counters);
+long q8_gemm_xs_bytes(long cols, long t);
+long q8_gemm_part_floats(long rows, long cols, long t);
+/* the kernel's choice for a shape: MG token tiles, RT row tiles a wave, KP pairs of blocks and NW
+ * waves a workgroup, ks workgroups along K, cps ranges of KP pairs a workgroup */
+void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *nw, int *ks, int *cps);
 /* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
 void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
 /* GGUF Q8_0 rows to form S, both device. */

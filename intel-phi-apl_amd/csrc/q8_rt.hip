@@ -60,9 +60,17 @@ struct ctx {
     /* staging for the host-pointer products: pinned host and device, in floats */
     float *hx = nullptr, *hy = nullptr, *dx = nullptr, *dy = nullptr;
     size_t x_cap = 0, y_cap = 0;
-    /* scratch for the exact fused pair: G and U */
+    /* scratch for the fused pair when it runs as two products (exact mode, t >= 5): G and U */
     float *scratch = nullptr;
     size_t scratch_cap = 0;
+    /* the matrix-core product's workspace: x limbs, K-split partials, per-tile counters */
+    void *xs = nullptr;
+    size_t xs_cap = 0;
+    float *part = nullptr;
+    uint32_t *counters = nullptr;
+    /* buffers replaced by larger ones: a recorded graph may still use them, so they live
+     * until rt_fini */
+    std::vector<void *> retired;
     std::unordered_map<const void *, matrix> weights;
     job queue[RT_BATCH];
     int queued = 0;
@@ -133,15 +141,62 @@ void reserve_staging(ctx *c, size_t nx, size_t ny)
     }
 }
 
+/* Workspace is allocated on demand, never while the stream is being recorded into a graph:
+ * a product of a new, larger size must run once before a graph records it. */
+void no_capture(ctx *c, const char *what)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    HIPCHECK(hipStreamIsCapturing(c->stream, &st));
+    if (st != hipStreamCaptureStatusNone) {
+        fprintf(stderr, "q8_rt: %s must grow while a graph is being recorded: run a product of this size once before rt_graph_begin\n", what);
+        abort();
+    }
+}
+
 float *reserve_scratch(ctx *c, size_t n)
 {
     if (n > c->scratch_cap) {
+        no_capture(c, "the fused pair's scratch");
         if (c->scratch)
-            HIPCHECK(hipFree(c->scratch));
+            c->retired.push_back(c->scratch);
         HIPCHECK(hipMalloc((void **)&c->scratch, n * sizeof(float)));
         c->scratch_cap = n;
     }
     return c->scratch;
+}
+
+void reserve_gemm(ctx *c, long rows, long cols, long t)
+{
+    const size_t xb = (size_t)q8_gemm_xs_bytes(cols, t);
+    if (xb > c->xs_cap) {
+        no_capture(c, "the matrix-core product's x workspace");
+        if (c->xs)
+            c->retired.push_back(c->xs);
+        HIPCHECK(hipMalloc(&c->xs, xb));
+        c->xs_cap = xb;
+    }
+    if (!c->part && q8_gemm_part_floats(rows, cols, t) > 0) {
+        no_capture(c, "the matrix-core product's partial sums");
+        HIPCHECK(hipMalloc((void **)&c->part, (size_t)Q8_GEMM_PART_MAX * sizeof(float)));
+        HIPCHECK(hipMalloc((void **)&c->counters, Q8_GEMM_COUNTERS * sizeof(uint32_t)));
+        HIPCHECK(hipMemsetAsync(c->counters, 0, Q8_GEMM_COUNTERS * sizeof(uint32_t), c->stream));
+    }
+    if (q8_gemm_part_floats(rows, cols, t) > Q8_GEMM_PART_MAX)
+        fail("the matrix-core product", "its K-split partials exceed the workspace (a planning error)");
+}
+
+/* Y = X W^T for t >= 5 tokens, 64 at a time */
+void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, long xs, long t, float *y)
+{
+    for (long k = 0; k < t; k += 64) {
+        const long n = t - k < 64 ? t - k : 64;
+        if (n <= 4) {
+            q8_launch_gemv((q8_stream_t)c->stream, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows);
+            continue;
+        }
+        reserve_gemm(c, rows, cols, n);
+        q8_launch_gemm_mfma((q8_stream_t)c->stream, w, rows, cols, x + k * xs, xs, n, y + k * rows, c->xs, c->part, c->counters);
+    }
 }
 
 void launched(const char *what)
@@ -175,10 +230,16 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
         launched("the reference-order product");
         return;
     }
-    if (t <= 4)
+    if (t <= 4) {
         q8_launch_gemv(s, w0, w1, rows, cols, x, xs, t, y);
-    else
-        q8_launch_gemm(s, w0, w1, rows, cols, x, xs, t, y);
+    } else if (!w1) {
+        gemm_tokens(c, w0, rows, cols, x, xs, t, y);
+    } else {
+        float *g = reserve_scratch(c, (size_t)(2 * rows * t));
+        gemm_tokens(c, w0, rows, cols, x, xs, t, g);
+        gemm_tokens(c, w1, rows, cols, x, xs, t, g + rows * t);
+        q8_launch_swiglu_ew(s, g, g + rows * t, rows * t, y);
+    }
     launched("the product");
 }
 
@@ -275,6 +336,14 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipFree(c->dy));
     if (c->scratch)
         HIPCHECK(hipFree(c->scratch));
+    if (c->xs)
+        HIPCHECK(hipFree(c->xs));
+    if (c->part)
+        HIPCHECK(hipFree(c->part));
+    if (c->counters)
+        HIPCHECK(hipFree(c->counters));
+    for (void *p : c->retired)
+        HIPCHECK(hipFree(p));
     for (auto &e : c->kt_events)
         HIPCHECK(hipEventDestroy(e));
     HIPCHECK(hipEventDestroy(c->ev0));

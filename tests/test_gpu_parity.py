@@ -217,6 +217,83 @@ def test_fused_gate_up(rt, oracle, t):
     assert_parity(ex, want, f"exact swiglu t={t}")
 
 
+@pytest.mark.parametrize("rows,cols,t", [(1888, 512, 16), (48, 4096, 33), (16, 1024, 5), (4096, 12288, 64), (1024, 2048, 100), (6144, 4096, 24),
+                                         (256, 256, 47)])
+def test_matrix_core_gemm_shapes(rt, oracle, rows, cols, t):
+    """The matrix-core product at row counts that leave a partial workgroup (1888, 48, 16), every token
+    tile count (5..64), more than 64 tokens (two launches), and heavy-tailed scales on one case; the K
+    split's partials are summed by the last workgroup of each row tile."""
+    dist = "lognormal" if t == 24 else "normal"
+    q8, x = synth.case(rows * 3 + cols + t, rows, cols, t, dist)
+    say("mfma gemm", rows, cols, t, dist)
+    got = gpu_gemm(rt, q8, rows, cols, x)
+    m = assert_parity(got, oracle.gemm_f64(q8, rows, cols, x), f"{rows}x{cols} t={t}")
+    say("  ", m)
+
+
+def test_matrix_core_gemm_deterministic(rt):
+    """The K-split sums partials in split order: repeated products give the same bits."""
+    rows, cols, t = 4096, 12288, 16
+    q8, x = synth.case(17, rows, cols, t)
+    w = rt.upload(q8, rows, cols)
+    ys = [gpu_gemm(rt, q8, rows, cols, x, w=w) for _ in range(3)]
+    rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+    for y in ys[1:]:
+        assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
+
+
+def test_fused_pair_many_tokens(rt, oracle):
+    """rt_gemv_swiglu_dev at t >= 5 (two matrix-core products and the SiLU(g)*u epilogue)."""
+    rows, cols, t = 2048, 2048, 8
+    rng = np.random.default_rng(77)
+    q8g, q8u = synth.q8_rows(rng, rows, cols), synth.q8_rows(rng, rows, cols)
+    x = synth.x_f32(rng, t, cols)
+    got = gpu_swiglu(rt, q8g, q8u, rows, cols, x)
+    want = oracle.swiglu_f64(oracle.gemm_f64(q8g, rows, cols, x), oracle.gemm_f64(q8u, rows, cols, x))
+    assert_parity(got, want, "swiglu t=8")
+
+
+def test_graph_replays_match_eager(rt):
+    """A recorded sequence (decode products, the fused pair and a K-split matrix-core product, which
+    resets its own counters) replayed three times, with eager work between the replays, gives the
+    eager result bit for bit every time."""
+    rng = np.random.default_rng(8)
+    rows, cols, t = 2048, 4096, 16
+    mats = [synth.q8_rows(rng, rows, cols) for _ in range(3)]
+    x = synth.x_f32(rng, t, cols)
+    ws = [rt.upload(m, rows, cols) for m in mats]
+    with Dev(rt) as d:
+        dx = d.put(x)
+        y1, y2, y3 = d.empty(4 * rows), d.empty(4 * 2 * rows), d.empty(4 * t * rows)
+        yz = d.empty(4 * t * rows)
+
+        def seq():
+            rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[0]), rows, cols, c.c_void_p(dx), cols, 1, c.c_void_p(y1))
+            rt.lib.rt_gemv_swiglu_dev(rt.R, c.c_void_p(ws[1]), c.c_void_p(ws[2]), rows, cols, c.c_void_p(dx), cols, 2, c.c_void_p(y2))
+            rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[2]), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(y3))
+
+        seq()
+        want = [d.get(p, n, np.float32) for p, n in ((y1, rows), (y2, 2 * rows), (y3, t * rows))]
+        rt.lib.rt_graph_begin(rt.R)
+        seq()
+        g = rt.lib.rt_graph_end(rt.R)
+        try:
+            for rep in range(3):
+                for p, n in ((y1, rows), (y2, 2 * rows), (y3, t * rows)):
+                    rt.to_dev(p, np.zeros(n, np.float32))
+                rt.lib.rt_graph_launch(rt.R, c.c_void_p(g))
+                got = [d.get(p, n, np.float32) for p, n in ((y1, rows), (y2, 2 * rows), (y3, t * rows))]
+                for a, b in zip(got, want):
+                    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep}"
+                # eager work between replays: another K-split product on the same workspace
+                rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[0]), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(yz))
+                rt.sync()
+        finally:
+            rt.lib.rt_graph_free(rt.R, c.c_void_p(g))
+            for w in ws:
+                rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
 def test_exact_kernels_at_config_shapes(rt, oracle):
     """Bit-identical to the oracle (the reference's order) at the 9B shapes, tokens 1 and 3."""
     for rows, cols, t in [(4096, 12288, 1), (6144, 4096, 3)]:
