@@ -18,6 +18,7 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "q8_device.h"
 
@@ -133,38 +134,23 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_s(const uint8_t *__restr
     }
 }
 
-/* The decode kernel for cols % 1024 == 0: a workgroup of NW waves owns RW rows (one group's
- * quarter) and all of K; wave w takes the K-slice [w*1024*S, (w+1)*1024*S), S steps of 64
- * 16-column units. Every load of a lane (P*RW*S weight units and their scales, then x) is
- * issued before any arithmetic, so the whole matrix is in flight in the first round trip: the
- * small layer matrices are latency-bound otherwise. Then per lane the same arithmetic as
- * gemv_s; the lanes' partials summed by q8_wave_sum_dpp, the waves' in LDS in wave order. */
-template <int MT, int RW, int S, int PAIR>
-__global__ __launch_bounds__(256) void gemv_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
-                                              const float *__restrict__ x, long x_stride, float *__restrict__ y)
+/* The decode kernel for cols % 1024 == 0: a workgroup of NW waves owns RW rows and all of K;
+ * wave w takes the K-slice [w*1024*S, (w+1)*1024*S), S steps of 64 16-column units (lane l:
+ * units l + 64 s). Every load of a lane is issued before any arithmetic, x first and then the
+ * weights row by row (loads retire in order, so row r's arithmetic waits for rows 0..r only), so
+ * the whole matrix is in flight in the first round trip: the layer matrices are latency-bound
+ * otherwise. Per unit: 16 exact int8->f32 converts shared by the MT tokens, a 16-step fma chain
+ * per token, then acc = fma(s, d, acc) with the unit's block scale. The lanes' partials are summed
+ * by q8_wave_sum_dpp, the NW waves' in LDS in wave order: the same order every run. */
+template <int MT, int RW, int S, int NW, int PAIR>
+__global__ __launch_bounds__(64 * NW) void gemv_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
+                                                  const float *__restrict__ x, long x_stride, float *__restrict__ y)
 {
     constexpr int P = PAIR + 1;
-    __shared__ float red[4][P * RW * MT];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long r0 = (long)blockIdx.x * RW;
     const long u0 = (long)wave * 64 * S + lane;
 
-    uint4 q[P][RW][S];
-    uint16_t dh[P][RW][S];
-#pragma unroll
-    for (int p = 0; p < P; p++) {
-        const uint8_t *w = p ? w1 : w0;
-#pragma unroll
-        for (int r = 0; r < RW; r++) {
-            const uint8_t *wq = w + q8s_row_q(r0 + r, cols);
-            const uint16_t *wd = (const uint16_t *)(w + q8s_row_d(r0 + r, cols));
-#pragma unroll
-            for (int s = 0; s < S; s++) {
-                q[p][r][s] = *(const uint4 *)(wq + 16 * (u0 + 64 * s));
-                dh[p][r][s] = wd[(u0 + 64 * s) >> 1];
-            }
-        }
-    }
     float4 xv[MT][S][4];
 #pragma unroll
     for (int m = 0; m < MT; m++)
@@ -173,48 +159,67 @@ __global__ __launch_bounds__(256) void gemv_k(const uint8_t *__restrict__ w0, co
 #pragma unroll
             for (int c = 0; c < 4; c++)
                 xv[m][s][c] = *(const float4 *)(x + m * x_stride + 16 * (u0 + 64 * s) + 4 * c);
+    uint4 q[RW][P][S];
+    uint16_t dh[RW][P][S];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const uint8_t *w = p ? w1 : w0;
+            const uint8_t *wq = w + q8s_row_q(r0 + r, cols);
+            const uint16_t *wd = (const uint16_t *)(w + q8s_row_d(r0 + r, cols));
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                q[r][p][s] = *(const uint4 *)(wq + 16 * (u0 + 64 * s));
+                dh[r][p][s] = wd[(u0 + 64 * s) >> 1];
+            }
+        }
 
-    float acc[P][RW][MT];
+    float acc[RW][P][MT];
 #pragma unroll
-    for (int p = 0; p < P; p++)
-#pragma unroll
-        for (int r = 0; r < RW; r++)
-#pragma unroll
-            for (int m = 0; m < MT; m++)
-                acc[p][r][m] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < S; s++)
+    for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int r = 0; r < RW; r++) {
-                const uint32_t qw[4] = {q[p][r][s].x, q[p][r][s].y, q[p][r][s].z, q[p][r][s].w};
-                float wf[16];
+            for (int m = 0; m < MT; m++) {
+                acc[r][p][m] = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 16; j++)
-                    wf[j] = q8_s8(qw[j >> 2], j & 3);
-                const float d = q8_half(dh[p][r][s]);
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
+                for (int s = 0; s < S; s++) {
+                    const uint32_t qw[4] = {q[r][p][s].x, q[r][p][s].y, q[r][p][s].z, q[r][p][s].w};
                     const float xs[16] = {xv[m][s][0].x, xv[m][s][0].y, xv[m][s][0].z, xv[m][s][0].w, xv[m][s][1].x, xv[m][s][1].y,
                                           xv[m][s][1].z, xv[m][s][1].w, xv[m][s][2].x, xv[m][s][2].y, xv[m][s][2].z, xv[m][s][2].w,
                                           xv[m][s][3].x, xv[m][s][3].y, xv[m][s][3].z, xv[m][s][3].w};
                     float sum = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 16; j++)
-                        sum = __builtin_fmaf(wf[j], xs[j], sum);
-                    acc[p][r][m] = __builtin_fmaf(sum, d, acc[p][r][m]);
+                        sum = __builtin_fmaf(q8_s8(qw[j >> 2], j & 3), xs[j], sum);
+                    acc[r][p][m] = __builtin_fmaf(sum, q8_half(dh[r][p][s]), acc[r][p][m]);
                 }
             }
-#pragma unroll
-    for (int p = 0; p < P; p++)
+    if (NW == 1) {
 #pragma unroll
         for (int r = 0; r < RW; r++)
 #pragma unroll
             for (int m = 0; m < MT; m++) {
-                const float v = q8_wave_sum_dpp(acc[p][r][m]);
+                float v[P];
+#pragma unroll
+                for (int p = 0; p < P; p++)
+                    v[p] = q8_wave_sum_dpp(acc[r][p][m]);
                 if (lane == 0)
-                    red[wave][(p * RW + r) * MT + m] = v;
+                    y[m * rows + r0 + r] = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
+            }
+        return;
+    }
+    __shared__ float red[NW][RW * P * MT];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const float v = q8_wave_sum_dpp(acc[r][p][m]);
+                if (lane == 0)
+                    red[wave][(r * P + p) * MT + m] = v;
             }
     __syncthreads();
     if (threadIdx.x < RW * MT) {
@@ -222,42 +227,87 @@ __global__ __launch_bounds__(256) void gemv_k(const uint8_t *__restrict__ w0, co
         float v[P];
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            v[p] = red[0][(p * RW + r) * MT + m];
-            for (int w = 1; w < nw; w++)
-                v[p] += red[w][(p * RW + r) * MT + m];
+            v[p] = red[0][(r * P + p) * MT + m];
+#pragma unroll
+            for (int k = 1; k < NW; k++)
+                v[p] += red[k][(r * P + p) * MT + m];
         }
         y[m * rows + r0 + r] = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
     }
 }
 
-template <int MT, int RW, int PAIR>
-static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y)
+/* Q8_GEMV_CFG = "RW,NW" overrides the decode kernel's rows and waves a workgroup, for tuning sweeps. */
+static bool gemv_env(int *rw, int *nw)
 {
-    const long kb = cols / 1024;
-    const int nw = cols % 1024 ? 0 : kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
-    const long steps = nw ? kb / nw : 0;
-    const dim3 grid((unsigned)(rows / RW)), block(64 * nw);
-    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
-    switch (steps) {
-    case 1: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 1, PAIR), (gemv_k<MT, RW, 1, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    case 2: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 2, PAIR), (gemv_k<MT, RW, 2, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    case 3: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 3, PAIR), (gemv_k<MT, RW, 3, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    case 4: Q8_LAUNCH(q8_time_name("gemv_k", 4, MT, RW, 4, PAIR), (gemv_k<MT, RW, 4, PAIR>), grid, block, s, a, b, rows, cols, x, xs, y); return;
-    default: break;
+    static int cached = -1, crw = 0, cnw = 0;
+    if (cached < 0) {
+        const char *v = getenv("Q8_GEMV_CFG");
+        cached = v && sscanf(v, "%d,%d", &crw, &cnw) == 2 ? 1 : 0;
     }
-    /* any other cols (a multiple of 32): the loop over K */
-    const long waves = rows / RW;
-    Q8_LAUNCH(q8_time_name("gemv_s", 3, MT, RW, PAIR), (gemv_s<MT, RW, PAIR>), dim3((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), s, a, b, rows, cols, x, xs, y);
+    *rw = crw, *nw = cnw;
+    return cached == 1;
 }
 
-template <int RW, int PAIR>
+template <int MT, int RW, int S, int NW, int PAIR>
+static void gemv_launch(hipStream_t s, const uint8_t *a, const uint8_t *b, long rows, long cols, const float *x, long xs, float *y)
+{
+    Q8_LAUNCH(q8_time_name("gemv_k", 5, MT, RW, S, NW, PAIR), (gemv_k<MT, RW, S, NW, PAIR>), dim3((unsigned)(rows / RW)), dim3(64 * NW), s, a, b, rows,
+              cols, x, xs, y);
+}
+
+/* K = 1024 * S * NW; RW rows a workgroup (rows % RW == 0) */
+template <int MT, int RW, int PAIR>
+static bool gemv_go_rw(hipStream_t s, int nw, long kb, const uint8_t *a, const uint8_t *b, long rows, long cols, const float *x, long xs, float *y)
+{
+#define K1(S, N)                                                                                                       \
+    if (nw == N && kb == (long)S * N) {                                                                                \
+        gemv_launch<MT, RW, S, N, PAIR>(s, a, b, rows, cols, x, xs, y);                                                \
+        return true;                                                                                                   \
+    }
+    K1(1, 1) K1(1, 2) K1(1, 4) K1(1, 6) K1(1, 8) K1(1, 12) K1(1, 16) K1(2, 4) K1(3, 4) K1(4, 4) K1(2, 2) K1(3, 2) K1(2, 1) K1(2, 8)
+#undef K1
+    return false;
+}
+
+template <int MT, int PAIR>
+static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y)
+{
+    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
+    const long kb = cols % 1024 ? 0 : cols / 1024;
+    /* measured on the 9B shapes: 8 rows a workgroup (4 for the pair: the same 8 rows of loads a
+     * lane), one 1024-column step a wave, so K = 4096 takes 4 waves and K = 12288 takes 12 */
+    int rw = PAIR ? 4 : 8, nw = kb;
+    if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
+        nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
+    int erw, enw;
+    if (gemv_env(&erw, &enw))
+        rw = erw, nw = enw;
+    if (kb && rows % rw == 0) {
+        bool done = false;
+        switch (rw) {
+        case 1: done = gemv_go_rw<MT, 1, PAIR>(s, nw, kb, a, b, rows, cols, x, xs, y); break;
+        case 2: done = gemv_go_rw<MT, 2, PAIR>(s, nw, kb, a, b, rows, cols, x, xs, y); break;
+        case 8: done = gemv_go_rw<MT, 8, PAIR>(s, nw, kb, a, b, rows, cols, x, xs, y); break;
+        case 16: done = gemv_go_rw<MT, 16, PAIR>(s, nw, kb, a, b, rows, cols, x, xs, y); break;
+        default: done = rw == 4 && gemv_go_rw<MT, 4, PAIR>(s, nw, kb, a, b, rows, cols, x, xs, y); break;
+        }
+        if (done)
+            return;
+    }
+    /* any other cols (a multiple of 32): the loop over K */
+    const long waves = rows / 4;
+    Q8_LAUNCH(q8_time_name("gemv_s", 3, MT, 4, PAIR), (gemv_s<MT, 4, PAIR>), dim3((unsigned)((waves + GEMV_WAVES - 1) / GEMV_WAVES)), dim3(64 * GEMV_WAVES), s,
+              a, b, rows, cols, x, xs, y);
+}
+
+template <int PAIR>
 static void gemv_t(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y)
 {
     switch (t) {
-    case 1: gemv_go<1, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
-    case 2: gemv_go<2, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
-    case 3: gemv_go<3, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
-    default: gemv_go<4, RW, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    case 1: gemv_go<1, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    case 2: gemv_go<2, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    case 3: gemv_go<3, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
+    default: gemv_go<4, PAIR>(s, w0, w1, rows, cols, x, xs, y); break;
     }
 }
 
@@ -268,9 +318,9 @@ void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long row
     for (long k = 0; k < t; k += 4) {
         const long n = t - k < 4 ? t - k : 4;
         if (w1)
-            gemv_t<4, 1>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
+            gemv_t<1>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
         else
-            gemv_t<4, 0>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
+            gemv_t<0>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
     }
 }
 
