@@ -257,6 +257,43 @@ def verify_path(b):
     return out
 
 
+def deltanet_round(b):
+    """The 9B DeltaNet quartet (QKV 8192x4096, GATE 4096x4096, BETA and ALPHA 32x4096, sharing x;
+    src/apl/qwen35.apl:93-96) over 32 layers of distinct weights, recorded as a graph: four launches
+    a layer against one round launch a layer (rt_gemv_round_dev)."""
+    shapes = [8192, 4096, 32, 32]
+    layers = [[b.matrix(r, HIDDEN) for r in shapes] for _ in range(LAYERS)]
+    x = b.vec(HIDDEN)
+    ys = [b.vec(r) for r in shapes]
+    per = LAYERS * sum(alg_bytes(r, HIDDEN, 1) for r in shapes) - LAYERS * 3 * 4 * HIDDEN  # x read once a round
+    R = (c.c_long * 4)(*shapes)
+    Y = (c.c_void_p * 4)(*ys)
+    Ws = [(c.c_void_p * 4)(*L) for L in layers]
+
+    def singles():
+        for L in layers:
+            for w, r, y in zip(L, shapes, ys):
+                b.gemm(w, r, HIDDEN, x, 1, y)
+
+    def rounds():
+        for W in Ws:
+            b.lib.rt_gemv_round_dev(b.R, 4, W, R, HIDDEN, c.c_void_p(x), HIDDEN, 1, Y)
+
+    out = {"bytes": per}
+    for key, fn in (("four_launches", singles), ("one_round", rounds)):
+        b.lib.rt_graph_begin(b.R)
+        fn()
+        g = b.lib.rt_graph_end(b.R)
+        b.lib.rt_graph_launch(b.R, c.c_void_p(g))
+        ms = b.timed(lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(g)), 20)
+        b.lib.rt_graph_free(b.R, c.c_void_p(g))
+        out[key] = {"us_per_32_layers": round(1e3 * ms, 2), "GB/s": round(per / ms / 1e6, 1)}
+    for L in layers:
+        for w in L:
+            b.rt.free(w)
+    return out
+
+
 def layers_2b(b):
     """Config 2: 24 layers of QKV 3072x2048, out 2048x2048, gate/up 6144x2048 (fused), down 2048x6144."""
     H, F, Q = 2048, 6144, 2048 + 2 * 512
@@ -475,7 +512,7 @@ def main():
     name, cus = b.rt.device_info()
     log(f"device: {name}, {cus} CUs")
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
-                ("2b_layer_set", layers_2b))
+                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round))
     if a.only:
         want = a.only.split(",")
         for key, fn in sections:

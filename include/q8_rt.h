@@ -116,6 +116,11 @@ void rt_q8_free(struct rt *R, const void *w);
 void rt_gemv_dev(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
 /* Y = X W^T, t tokens (1..64), X rows x_stride floats apart (x_stride >= cols, % 4 == 0). */
 void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* A round of n (1..RT_BATCH) products sharing x, none reading another's y: y[i] = X w[i]^T,
+ * w[i] [rows[i] cols], as one launch where the kernel takes the shape (t <= 4), else one after
+ * another. The device form of rt_gemv_q x n + rt_gemv_go, which uses the same launch for queued
+ * decode products that share x (the DeltaNet quartet QKV/GATE/BETA/ALPHA, src/apl/qwen35.apl:93-96). */
+void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
 /* The FFN's fused pair: Y[k] = SiLU(G[k]) * U[k] with G = X Wg^T and U = X Wu^T, both [rows cols],
  * x read once for both; SiLU(g) = g / (1 + exp(-g)) (src/apl/qwen35.apl:38, 125). t tokens. */
 void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y);
@@ -177,6 +182,7 @@ float rt_timer_stop(struct rt *R);
 #define RT_K_GEMM 2      /* t >= 5, the matrix-core kernel */
 #define RT_K_GEMM_PAIR 3
 #define RT_K_EXACT 4 /* the reference-order kernel */
+#define RT_K_ROUND 5 /* a round of products sharing x, one launch (rows: their sum) */
 void rt_ktime(struct rt *R, int on);
 long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, char *names, long *grid, long max);
 

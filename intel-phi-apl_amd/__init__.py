@@ -45,6 +45,7 @@ _SIGS = {
     "rt_gemv_dev": (None, [_vp, _vp, _long, _long, _vp, _vp]),
     "rt_gemm_dev": (None, [_vp, _vp, _long, _long, _vp, _long, _long, _vp]),
     "rt_gemv_swiglu_dev": (None, [_vp, _vp, _vp, _long, _long, _vp, _long, _long, _vp]),
+    "rt_gemv_round_dev": (None, [_vp, _int, _vp, _vp, _long, _vp, _long, _long, _vp]),
     "rt_dev_alloc": (_vp, [_vp, _long]),
     "rt_dev_free": (None, [_vp, _vp]),
     "rt_dev_upload": (None, [_vp, _vp, _vp, _long]),
@@ -67,7 +68,7 @@ _SIGS = {
     "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _long]),
 }
 
-KINDS = {0: "gemv", 1: "gemv_pair", 2: "gemm", 3: "gemm_pair", 4: "exact"}
+KINDS = {0: "gemv", 1: "gemv_pair", 2: "gemm", 3: "gemm_pair", 4: "exact", 5: "round"}
 
 
 def header_symbols(path=HEADER):

@@ -116,6 +116,17 @@ extern long *q8_next_grid;
 
 /* Y = X W^T, t tokens, the fast kernels; W form S. w1 != NULL: the fused pair, Y = SiLU(X W0^T) * (X W1^T). */
 void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* A round of products sharing x as one launch (t <= 4, cols % 1024 == 0, every rows % 8 == 0):
+ * 0, or -1 (nothing launched: the caller runs them one by one). */
+#define Q8_ROUND_MAX 8
+struct q8_round {
+    int n;
+    const void *w[Q8_ROUND_MAX];
+    float *y[Q8_ROUND_MAX];
+    long rows[Q8_ROUND_MAX];
+    long start[Q8_ROUND_MAX + 1]; /* first workgroup of each product; start[n] = the grid */
+};
+int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
 /* The reference's order, every y bit-identical to the reference's F32 host path. */
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* Y = X W^T for 5 <= t <= 64 on the matrix cores: the x limb pass, then the product. xs holds

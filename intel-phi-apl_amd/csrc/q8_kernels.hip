@@ -143,12 +143,11 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_s(const uint8_t *__restr
  * per token, then acc = fma(s, d, acc) with the unit's block scale. The lanes' partials are summed
  * by q8_wave_sum_dpp, the NW waves' in LDS in wave order: the same order every run. */
 template <int MT, int RW, int S, int NW, int PAIR>
-__global__ __launch_bounds__(64 * NW) void gemv_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
-                                                  const float *__restrict__ x, long x_stride, float *__restrict__ y)
+__device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols, const float *__restrict__ x,
+                                          long x_stride, float *__restrict__ y, long r0)
 {
     constexpr int P = PAIR + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const long r0 = (long)blockIdx.x * RW;
     const long u0 = (long)wave * 64 * S + lane;
 
     float4 xv[MT][S][4];
@@ -234,6 +233,27 @@ __global__ __launch_bounds__(64 * NW) void gemv_k(const uint8_t *__restrict__ w0
         }
         y[m * rows + r0 + r] = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
     }
+}
+
+template <int MT, int RW, int S, int NW, int PAIR>
+__global__ __launch_bounds__(64 * NW) void gemv_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
+                                                  const float *__restrict__ x, long x_stride, float *__restrict__ y)
+{
+    gemv_body<MT, RW, S, NW, PAIR>(w0, w1, rows, cols, x, x_stride, y, (long)blockIdx.x * RW);
+}
+
+/* A round of up to Q8_ROUND_MAX products that share x (the reference's queued products, none
+ * reading another's result, src/card/rt.c:216-242), as one launch: workgroup b belongs to the
+ * product p with start[p] <= b < start[p+1] and takes its rows [(b - start[p]) * RW, +RW). */
+template <int MT, int RW, int S, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_round(q8_round r, long cols, const float *__restrict__ x, long x_stride)
+{
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < Q8_ROUND_MAX; k++)
+        if (k < r.n && (long)blockIdx.x >= r.start[k])
+            p = k;
+    gemv_body<MT, RW, S, NW, 0>((const uint8_t *)r.w[p], nullptr, r.rows[p], cols, x, x_stride, r.y[p], ((long)blockIdx.x - r.start[p]) * RW);
 }
 
 /* Q8_GEMV_CFG = "RW,NW" overrides the decode kernel's rows and waves a workgroup, for tuning sweeps. */
@@ -322,6 +342,50 @@ void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long row
         else
             gemv_t<0>(s, w0, w1, rows, cols, x + k * x_stride, x_stride, n, y + k * rows);
     }
+}
+
+template <int MT, int RW>
+static bool round_go(hipStream_t s, int nw, long kb, const q8_round &r, long cols, const float *x, long xs)
+{
+#define K1(S, N)                                                                                                       \
+    if (nw == N && kb == (long)S * N) {                                                                                \
+        Q8_LAUNCH(q8_time_name("gemv_round", 4, MT, RW, S, N), (gemv_round<MT, RW, S, N>), dim3((unsigned)r.start[r.n]), dim3(64 * N), s, r, cols, x,  \
+                  xs);                                                                                                 \
+        return true;                                                                                                   \
+    }
+    K1(1, 1) K1(1, 2) K1(1, 4) K1(1, 6) K1(1, 8) K1(1, 12) K1(1, 16) K1(2, 4) K1(3, 4) K1(4, 4)
+#undef K1
+    return false;
+}
+
+int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y)
+{
+    const long kb = cols % 1024 ? 0 : cols / 1024;
+    if (n < 1 || n > Q8_ROUND_MAX || t < 1 || t > 4 || !kb)
+        return -1;
+    constexpr int RW = 8;
+    int nw = kb;
+    if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
+        nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
+    q8_round r = {};
+    r.n = n;
+    for (int i = 0; i < n; i++) {
+        if (rows[i] % RW)
+            return -1;
+        r.w[i] = w[i];
+        r.y[i] = y[i];
+        r.rows[i] = rows[i];
+        r.start[i + 1] = r.start[i] + rows[i] / RW;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    bool done = false;
+    switch (t) {
+    case 1: done = round_go<1, RW>(s, nw, kb, r, cols, x, x_stride); break;
+    case 2: done = round_go<2, RW>(s, nw, kb, r, cols, x, x_stride); break;
+    case 3: done = round_go<3, RW>(s, nw, kb, r, cols, x, x_stride); break;
+    default: done = round_go<4, RW>(s, nw, kb, r, cols, x, x_stride); break;
+    }
+    return done ? 0 : -1;
 }
 
 /* ---------------------------------------------------------------- the reference's order */

@@ -243,7 +243,32 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
     launched("the product");
 }
 
-/* A round over host pointers: distinct x staged once, every product, every y back, one wait. */
+/* Products sharing x as one launch: true when launched, false when the kernel does not take the
+ * shape (the caller then runs them one by one). */
+bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long cols, const float *x, long xs, long t, float *const *y)
+{
+    const bool timed = c->ktime_on && c->kt.size() < KT_MAX;
+    if (timed) {
+        long total = 0;
+        for (int i = 0; i < n; i++)
+            total += rows[i];
+        const size_t k = c->kt.size();
+        c->kt.push_back(ktrec{RT_K_ROUND, total, cols, t, 0, {0}});
+        q8_time_next(c->kt_events[2 * k], c->kt_events[2 * k + 1], c->kt.back().name, &c->kt.back().grid);
+    }
+    if (q8_launch_gemv_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y) != 0) {
+        if (timed) {
+            q8_time_next(nullptr, nullptr, nullptr, nullptr);
+            c->kt.pop_back();
+        }
+        return false;
+    }
+    launched("the round");
+    return true;
+}
+
+/* A round over host pointers: distinct x staged once, every product (those sharing x as one
+ * launch), every y back, one wait. */
 void run_round(ctx *c, job *jobs, int n)
 {
     size_t nx = 0, ny = 0;
@@ -274,9 +299,27 @@ void run_round(ctx *c, job *jobs, int n)
             memcpy(c->hx + j.x_off, j.x, sizeof(float) * (size_t)(j.t * j.cols));
     }
     HIPCHECK(hipMemcpyAsync(c->dx, c->hx, nx * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    /* decode products that share x (and t): one launch for the group */
+    bool done[RT_BATCH] = {};
+    for (int i = 0; i < n && !c->exact; i++) {
+        if (done[i] || jobs[i].t > 4)
+            continue;
+        const void *w[RT_BATCH];
+        long rows[RT_BATCH];
+        float *y[RT_BATCH];
+        int idx[RT_BATCH], k = 0;
+        for (int j = i; j < n; j++)
+            if (!done[j] && jobs[j].x_off == jobs[i].x_off && jobs[j].t == jobs[i].t && jobs[j].cols == jobs[i].cols) {
+                w[k] = jobs[j].w, rows[k] = jobs[j].rows, y[k] = c->dy + jobs[j].y_off, idx[k++] = j;
+            }
+        if (k > 1 && round_launch(c, k, w, rows, jobs[i].cols, c->dx + jobs[i].x_off, jobs[i].cols, jobs[i].t, y))
+            for (int j = 0; j < k; j++)
+                done[idx[j]] = true;
+    }
     for (int i = 0; i < n; i++) {
         const job &j = jobs[i];
-        product(c, j.w, nullptr, j.rows, j.cols, c->dx + j.x_off, j.cols, j.t, c->dy + j.y_off);
+        if (!done[i])
+            product(c, j.w, nullptr, j.rows, j.cols, c->dx + j.x_off, j.cols, j.t, c->dy + j.y_off);
     }
     HIPCHECK(hipMemcpyAsync(c->hy, c->dy, ny * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIPCHECK(hipStreamSynchronize(c->stream));
@@ -490,6 +533,24 @@ void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float 
     if (t < 1 || x_stride < cols || x_stride % 4)
         fail("rt_gemm_dev", "t >= 1 and x_stride >= cols, a multiple of 4");
     product(c, w, nullptr, rows, cols, x, x_stride, t, y);
+}
+
+void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y)
+{
+    ctx *c = get(R, "rt_gemv_round_dev");
+    if (n < 1 || n > RT_BATCH || !w || !rows || !y)
+        fail("rt_gemv_round_dev", "needs 1..RT_BATCH (8) products");
+    check_dev_ptr("rt_gemv_round_dev", x, "x");
+    if (t < 1 || x_stride < cols || x_stride % 4)
+        fail("rt_gemv_round_dev", "t >= 1 and x_stride >= cols, a multiple of 4");
+    for (int i = 0; i < n; i++) {
+        check_shape(c, "rt_gemv_round_dev", w[i], rows[i], cols);
+        check_dev_ptr("rt_gemv_round_dev", y[i], "every y");
+    }
+    if (!c->exact && t <= 4 && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
+        return;
+    for (int i = 0; i < n; i++)
+        product(c, w[i], nullptr, rows[i], cols, x, x_stride, t, y[i]);
 }
 
 void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y)

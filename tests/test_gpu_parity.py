@@ -294,6 +294,35 @@ def test_graph_replays_match_eager(rt):
                 rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+@pytest.mark.parametrize("t", [1, 3])
+def test_round_one_launch_equals_singles(rt, oracle, t):
+    """The 9B DeltaNet quartet (QKV 8192x4096, GATE 4096x4096, BETA and ALPHA 32x4096, all reading H;
+    src/apl/qwen35.apl:93-96) as one launch (rt_gemv_round_dev) gives each product's bits as its own
+    launch does, and meets the parity bar."""
+    cols = 4096
+    shapes = [8192, 4096, 32, 32]
+    rng = np.random.default_rng(60 + t)
+    mats = [synth.q8_rows(rng, r, cols) for r in shapes]
+    x = synth.x_f32(rng, t, cols)
+    ws = [rt.upload(m, r, cols) for m, r in zip(mats, shapes)]
+    try:
+        singles = [gpu_gemm(rt, m, r, cols, x, w=w) for m, r, w in zip(mats, shapes, ws)]
+        with Dev(rt) as d:
+            dx = d.put(x)
+            ys = [d.empty(4 * t * r) for r in shapes]
+            W = (c.c_void_p * 4)(*ws)
+            R = (c.c_long * 4)(*shapes)
+            Y = (c.c_void_p * 4)(*ys)
+            rt.lib.rt_gemv_round_dev(rt.R, 4, W, R, cols, c.c_void_p(dx), cols, t, Y)
+            got = [d.get(p, (t, r), np.float32) for p, r in zip(ys, shapes)]
+        for g, s1, m, r in zip(got, singles, mats, shapes):
+            assert np.array_equal(g.view(np.uint32), s1.view(np.uint32)), r
+            assert_parity(g, oracle.gemm_f64(m, r, cols, x), f"round {r}x{cols} t={t}")
+    finally:
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
 def test_exact_kernels_at_config_shapes(rt, oracle):
     """Bit-identical to the oracle (the reference's order) at the 9B shapes, tokens 1 and 3."""
     for rows, cols, t in [(4096, 12288, 1), (6144, 4096, 3)]:
