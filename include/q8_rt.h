@@ -107,6 +107,11 @@ const void *rt_q8_upload_packed(struct rt *R, const void *packed, long rows, lon
 /* Frees an uploaded matrix. */
 void rt_q8_free(struct rt *R, const void *w);
 
+/* Row `row` of an uploaded matrix, dequantised: z[k] = q * d, exact (src/card/rt.h:85; rt.c:484-501,
+ * the embedding read). z host memory, cols floats; returns when z is valid. Like the reference's it
+ * takes no struct rt: it uses the runtime rt_init set up last. */
+void rt_q8_row(const void *w, long cols, long row, float *z);
+
 /* ---- activations already in HBM (additions: no copies, stream-ordered, no wait)
  *
  * x, y are device addresses (from rt_dev_alloc, or any HIP allocation on the device). The
@@ -124,6 +129,13 @@ void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *ro
 /* The FFN's fused pair: Y[k] = SiLU(G[k]) * U[k] with G = X Wg^T and U = X Wu^T, both [rows cols],
  * x read once for both; SiLU(g) = g / (1 + exp(-g)) (src/apl/qwen35.apl:38, 125). t tokens. */
 void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* z[i*cols ..] = row rows[i] of w dequantised, i < n (rows: device longs, each < the matrix's
+ * rows; z device). The embedding read of a batch of tokens. An addition. */
+void rt_q8_rows_dev(struct rt *R, const void *w, long cols, const long *rows, long n, float *z);
+/* *idx (device) = the greedy next token over a[0..n) (device): the lowest i whose bits equal the
+ * fmaxf fold of a, as the host's rt_maxv then rt_index_of give it (src/card/rt.c:137-165) for
+ * Next = {w index-of max/w} (src/apl/qwen35.apl:161). Deterministic. An addition. */
+void rt_argmax_dev(struct rt *R, const float *a, long n, long *idx);
 /* Device memory for activations, and copies to and from it on the runtime's stream. */
 void *rt_dev_alloc(struct rt *R, long bytes);
 void rt_dev_free(struct rt *R, void *p);

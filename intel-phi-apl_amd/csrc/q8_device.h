@@ -143,6 +143,12 @@ long q8_gemm_part_floats(long rows, long cols, long t);
 void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *nw, int *ks, int *cps);
 /* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
 void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
+/* z[i] = row rows[i] of w dequantised (q * d, exact), i < n; rows and z device arrays. */
+void q8_launch_rows(q8_stream_t stream, const void *w, long cols, const long *rows, long n, float *z);
+/* *out = the lowest i with a[i] bit-equal to the fmaxf fold of a[0..n); cm, ci hold
+ * q8_argmax_chunks(n) candidates. */
+long q8_argmax_chunks(long n);
+void q8_launch_argmax(q8_stream_t stream, const float *a, long n, float *cm, long *ci, long *out);
 /* GGUF Q8_0 rows to form S, both device. */
 void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, void *out);
 /* Synthetic GGUF rows and F32 values on the device. */

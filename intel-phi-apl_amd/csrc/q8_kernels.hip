@@ -16,6 +16,7 @@
  *   prims       the conversions above, lane by lane, for the known-answer gates. */
 #include <hip/hip_runtime.h>
 
+#include <limits.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -463,6 +464,105 @@ void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, 
 {
     const long n = rows * (cols / Q8_BLOCK);
     repack_s<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)q8, rows, cols, (uint8_t *)out);
+}
+
+/* ---------------------------------------------------------------- rows and the greedy next token */
+
+/* z[i][k] = q * d of row rows[i] (src/card/rt.c:484-501: q converted, times the block scale, one
+ * rounding; exact, since d*q has at most 19 significant bits). One thread per 4 columns. */
+__global__ __launch_bounds__(256) void q8_rows_k(const uint8_t *__restrict__ w, long cols, const long *__restrict__ rows, long n, float *__restrict__ z)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long per = cols / 4;
+    if (i >= n * per)
+        return;
+    const long k = i / per, c4 = 4 * (i % per);
+    const long r = rows[k];
+    const uint32_t q = *(const uint32_t *)(w + q8s_row_q(r, cols) + c4);
+    const float d = q8_half(((const uint16_t *)(w + q8s_row_d(r, cols)))[c4 / Q8_BLOCK]);
+    *(float4 *)(z + k * cols + c4) = make_float4(q8_s8(q, 0) * d, q8_s8(q, 1) * d, q8_s8(q, 2) * d, q8_s8(q, 3) * d);
+}
+
+void q8_launch_rows(q8_stream_t stream, const void *w, long cols, const long *rows, long n, float *z)
+{
+    const long m = n * (cols / 4);
+    q8_rows_k<<<dim3((unsigned)((m + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)w, cols, rows, n, z);
+}
+
+/* The greedy next token of the reference's Next = {w index-of max/w} (src/apl/qwen35.apl:161; the
+ * host's rt_maxv then rt_index_of, src/card/rt.c:137-165): m = the fmaxf fold of a, then the lowest
+ * i whose bits equal m's. Pass 1: each workgroup's 4096 elements give (its m, its lowest such i);
+ * pass 2, one workgroup: m over the candidates, then the lowest candidate i with m's bits. The
+ * workgroup holding the first index of the global maximum has that maximum as its own. */
+#define ARG_CHUNK 4096
+__device__ __forceinline__ void argmax_block(float m, long idx, float *sm, long *si, float *out_m, long *out_i)
+{
+    /* m: fmaxf over the block, in a fixed tree */
+    sm[threadIdx.x] = m;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o)
+            sm[threadIdx.x] = fmaxf(sm[threadIdx.x], sm[threadIdx.x + o]);
+        __syncthreads();
+    }
+    const float bm = sm[0];
+    __syncthreads();
+    /* the lowest index whose value has bm's bits */
+    si[threadIdx.x] = __builtin_bit_cast(uint32_t, m) == __builtin_bit_cast(uint32_t, bm) ? idx : LONG_MAX;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o)
+            si[threadIdx.x] = si[threadIdx.x] < si[threadIdx.x + o] ? si[threadIdx.x] : si[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        *out_m = bm, *out_i = si[0];
+}
+
+__global__ __launch_bounds__(256) void argmax1(const float *__restrict__ a, long n, float *__restrict__ cm, long *__restrict__ ci)
+{
+    __shared__ float sm[256];
+    __shared__ long si[256];
+    const long b0 = (long)blockIdx.x * ARG_CHUNK;
+    const long b1 = b0 + ARG_CHUNK < n ? b0 + ARG_CHUNK : n;
+    /* each thread: fmaxf of its elements, then the lowest of its indices with that value's bits */
+    float m = a[b0];
+    for (long i = b0 + threadIdx.x; i < b1; i += 256)
+        m = fmaxf(m, a[i]);
+    long idx = LONG_MAX;
+    for (long i = b0 + threadIdx.x; i < b1; i += 256)
+        if (__builtin_bit_cast(uint32_t, a[i]) == __builtin_bit_cast(uint32_t, m)) {
+            idx = i;
+            break;
+        }
+    /* a thread whose range does not hold its own m (the a[b0] start) offers no index */
+    argmax_block(idx == LONG_MAX ? a[b0] : m, idx, sm, si, cm + blockIdx.x, ci + blockIdx.x);
+}
+
+__global__ __launch_bounds__(256) void argmax2(const float *__restrict__ cm, const long *__restrict__ ci, long nc, long *__restrict__ out)
+{
+    __shared__ float sm[256];
+    __shared__ long si[256];
+    float m = cm[0];
+    for (long i = threadIdx.x; i < nc; i += 256)
+        m = fmaxf(m, cm[i]);
+    long idx = LONG_MAX;
+    for (long i = threadIdx.x; i < nc; i += 256)
+        if (__builtin_bit_cast(uint32_t, cm[i]) == __builtin_bit_cast(uint32_t, m)) {
+            idx = ci[i];
+            break;
+        }
+    float om;
+    argmax_block(idx == LONG_MAX ? cm[0] : m, idx, sm, si, &om, out);
+}
+
+long q8_argmax_chunks(long n) { return (n + ARG_CHUNK - 1) / ARG_CHUNK; }
+
+void q8_launch_argmax(q8_stream_t stream, const float *a, long n, float *cm, long *ci, long *out)
+{
+    const long nc = q8_argmax_chunks(n);
+    argmax1<<<dim3((unsigned)nc), 256, 0, (hipStream_t)stream>>>(a, n, cm, ci);
+    argmax2<<<1, 256, 0, (hipStream_t)stream>>>(cm, ci, nc, out);
 }
 
 /* ---------------------------------------------------------------- synthetic inputs */

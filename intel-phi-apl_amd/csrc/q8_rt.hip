@@ -68,6 +68,9 @@ struct ctx {
     size_t xs_cap = 0;
     float *part = nullptr;
     uint32_t *counters = nullptr;
+    /* the greedy next token's candidates */
+    void *amax = nullptr;
+    size_t amax_cap = 0;
     /* buffers replaced by larger ones: a recorded graph may still use them, so they live
      * until rt_fini */
     std::vector<void *> retired;
@@ -81,6 +84,9 @@ struct ctx {
 };
 
 constexpr size_t KT_MAX = 16384;
+
+/* The runtime rt_init set up last: rt_q8_row takes no struct rt (src/card/rt.h:85) and uses it. */
+ctx *current = nullptr;
 
 ctx *get(struct rt *R, const char *fn)
 {
@@ -358,6 +364,7 @@ int rt_init(struct rt *R, int threads)
     R->gemm_chain = nullptr;
     R->chain = c;
     R->threads = threads;
+    current = c;
     return 0;
 }
 
@@ -389,6 +396,10 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipFree(p));
     for (auto &e : c->kt_events)
         HIPCHECK(hipEventDestroy(e));
+    if (c->amax)
+        HIPCHECK(hipFree(c->amax));
+    if (current == c)
+        current = nullptr;
     HIPCHECK(hipEventDestroy(c->ev0));
     HIPCHECK(hipEventDestroy(c->ev1));
     HIPCHECK(hipStreamDestroy(c->stream));
@@ -622,6 +633,60 @@ void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed)
         fail("rt_f32_fill_dev", "needs dst and n > 0");
     q8_launch_fill_f32((q8_stream_t)c->stream, dst, n, seed);
     launched("the fill");
+}
+
+void rt_q8_row(const void *w, long cols, long row, float *z)
+{
+    ctx *c = current;
+    if (!c)
+        fail("rt_q8_row", "rt_init has not run");
+    auto it = c->weights.find(w);
+    if (it == c->weights.end())
+        fail("rt_q8_row", "w is not a handle from rt_q8_upload");
+    if (cols != it->second.cols || row < 0 || row >= it->second.rows || !z)
+        fail("rt_q8_row", "cols must be the matrix's and row one of its rows");
+    reserve_staging(c, 64, (size_t)cols);
+    long *dr = (long *)c->dx; /* the row index, staged where x goes */
+    *(long *)c->hx = row;
+    HIPCHECK(hipMemcpyAsync(dr, c->hx, sizeof(long), hipMemcpyHostToDevice, c->stream));
+    q8_launch_rows((q8_stream_t)c->stream, w, cols, dr, 1, c->dy);
+    launched("the row read");
+    HIPCHECK(hipMemcpyAsync(c->hy, c->dy, sizeof(float) * (size_t)cols, hipMemcpyDeviceToHost, c->stream));
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    memcpy(z, c->hy, sizeof(float) * (size_t)cols);
+}
+
+void rt_q8_rows_dev(struct rt *R, const void *w, long cols, const long *rows, long n, float *z)
+{
+    ctx *c = get(R, "rt_q8_rows_dev");
+    auto it = c->weights.find(w);
+    if (it == c->weights.end())
+        fail("rt_q8_rows_dev", "w is not a handle from rt_q8_upload");
+    if (cols != it->second.cols || n < 1 || !rows)
+        fail("rt_q8_rows_dev", "cols must be the matrix's and n >= 1");
+    check_dev_ptr("rt_q8_rows_dev", z, "z");
+    q8_launch_rows((q8_stream_t)c->stream, w, cols, rows, n, z);
+    launched("the row gather");
+}
+
+void rt_argmax_dev(struct rt *R, const float *a, long n, long *idx)
+{
+    ctx *c = get(R, "rt_argmax_dev");
+    if (!a || !idx || n < 1)
+        fail("rt_argmax_dev", "needs a, idx and n >= 1");
+    const size_t need = (size_t)q8_argmax_chunks(n) * (sizeof(float) + sizeof(long)) + 64;
+    if (need > c->amax_cap) {
+        no_capture(c, "the next token's candidates");
+        if (c->amax)
+            c->retired.push_back(c->amax);
+        HIPCHECK(hipMalloc(&c->amax, need));
+        c->amax_cap = need;
+    }
+    const long nc = q8_argmax_chunks(n);
+    long *ci = (long *)c->amax;
+    float *cm = (float *)(ci + nc);
+    q8_launch_argmax((q8_stream_t)c->stream, a, n, cm, ci, idx);
+    launched("the next token");
 }
 
 void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes)

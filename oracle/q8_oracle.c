@@ -345,3 +345,35 @@ void q8o_gate21(uint64_t out[7])
     free(f16);
     free(hs);
 }
+
+/* rt.c:484-501: the block's q converted to F32 and multiplied by the block scale (fma(1, d, +0)
+ * = d exactly), one rounding per weight, which is exact. */
+void q8o_row(const uint8_t *q8, long cols, long row, float *z)
+{
+    const long nb = cols / BLOCK;
+    const uint8_t *r = q8 + row * nb * BLOCK_BYTES;
+    for (long b = 0; b < nb; b++) {
+        const float d = block_scale(r + b * BLOCK_BYTES);
+        const int8_t *q = (const int8_t *)(r + b * BLOCK_BYTES + 2);
+        for (int i = 0; i < BLOCK; i++)
+            z[b * BLOCK + i] = (float)q[i] * d;
+    }
+}
+
+/* rt.c:137-150 (rt_maxv: fmaxf from a[0]) then rt.c:153-165 (rt_index_of: bit-identical match,
+ * the lowest index). */
+long q8o_next(const float *a, long n)
+{
+    float m = a[0];
+    for (long i = 0; i < n; i++)
+        m = fmaxf(m, a[i]);
+    uint32_t want;
+    memcpy(&want, &m, 4);
+    for (long i = 0; i < n; i++) {
+        uint32_t got;
+        memcpy(&got, a + i, 4);
+        if (got == want)
+            return i;
+    }
+    return n;
+}

@@ -25,6 +25,10 @@
  *                    fractions) and linearity in x
  *   q8o_repack_s     the device form's definition checked byte by byte on tiny shapes
  *                    against an independent index formula in the tests
+ *   q8o_row          bit for bit against the reference's rt_q8_row on form I (oracle/_ref),
+ *                    and against numpy's d * q
+ *   q8o_next         against the reference's rt_maxv + rt_index_of (oracle/_ref) on random,
+ *                    tied, NaN-holding and ragged arrays, and numpy's nanargmax
  * Nothing here is "parity unpinned". */
 #ifndef Q8_ORACLE_H
 #define Q8_ORACLE_H
@@ -51,6 +55,13 @@ void q8o_gemm_f64(const uint8_t *q8, long rows, long cols, const float *x, long 
 
 /* SiLU(g) * u in F64 (src/apl/qwen35.apl:38; docs/model.md:29: Sig = 1 / (1 + exp(min(700, -g)))). */
 void q8o_swiglu_f64(const double *g, const double *u, long n, double *y);
+
+/* Row `row` of GGUF Q8_0 rows dequantised: z[k] = (float)q * half(d), one rounding, exact
+ * (src/card/rt.c:484-501). */
+void q8o_row(const uint8_t *q8, long cols, long row, float *z);
+/* The greedy next token (src/card/rt.c:137-165, rt_maxv then rt_index_of; src/apl/qwen35.apl:161):
+ * m = fmaxf fold of a from a[0], then the lowest i whose bits equal m's (n when none). */
+long q8o_next(const float *a, long n);
 
 /* Form S (include/q8_rt.h): per 16-row group, 16*cols int8 row by row, then 16 rows of
  * cols/32 binary16 scales. */

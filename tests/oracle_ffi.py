@@ -42,6 +42,9 @@ class Oracle:
         L.q8o_gate21_arrays.argtypes = [_vp, _vp]
         L.q8o_hash.restype = c.c_uint64
         L.q8o_hash.argtypes = [_vp, _l]
+        L.q8o_row.argtypes = [_vp, _l, _l, _vp]
+        L.q8o_next.restype = _l
+        L.q8o_next.argtypes = [_vp, _l]
 
     def gemm(self, q8, rows, cols, x, threads=0):
         """Y [t rows] in the reference's F32 order; x [t cols] or [cols]."""
@@ -72,6 +75,15 @@ class Oracle:
         out = np.empty(rows * cols // 32 * 34, np.uint8)
         self.lib.q8o_repack_s(_p(q8), rows, cols, _p(out))
         return out
+
+    def row(self, q8, cols, row):
+        z = np.empty(cols, np.float32)
+        self.lib.q8o_row(_p(q8), cols, row, _p(z))
+        return z
+
+    def next(self, a):
+        a = np.ascontiguousarray(a, np.float32)
+        return self.lib.q8o_next(_p(a), a.size)
 
     def half(self, h):
         return self.lib.q8o_half(int(h))
@@ -125,6 +137,11 @@ class Reference:
         L.ref_team_destroy.argtypes = [_vp]
         L.ref_team_gemv_i.argtypes = [_vp, _vp, _l, _l, _vp, _vp]
         L.ref_team_gemm_i.argtypes = [_vp, _vp, _l, _l, _vp, _l, _vp]
+        L.rt_maxv.restype = c.c_float
+        L.rt_maxv.argtypes = [_vp, _l]
+        L.rt_index_of.restype = _l
+        L.rt_index_of.argtypes = [_vp, _l, c.c_float]
+        L.rt_q8_row.argtypes = [_vp, _l, _l, _vp]
 
     def gemm(self, q8, rows, cols, x):
         x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
@@ -137,6 +154,22 @@ class Reference:
         y = np.empty(rows, np.float32)
         self.lib.ref_gemv(_p(q8), rows, cols, _p(np.ascontiguousarray(x, np.float32)), _p(y))
         return y
+
+    def next(self, a):
+        """rt_maxv then rt_index_of, as the generated code's Next runs them (a padded to whole
+        16-lane blocks, as the runtime's arrays are, src/card/rt.h:5-8)."""
+        n = a.size
+        buf = np.zeros((n + 15) // 16 * 16 + 16, np.float32)
+        buf[:n] = a
+        m = self.lib.rt_maxv(_p(buf), n)
+        return self.lib.rt_index_of(_p(buf), n, m)
+
+    def row(self, q8, rows, cols, row):
+        """rt_q8_row on the form I repack of GGUF rows."""
+        fi = self.repack_i(q8, rows, cols)
+        z = np.empty(cols + 16, np.float32)
+        self.lib.rt_q8_row(_p(fi), cols, row, _p(z))
+        return z[:cols]
 
     def repack_i(self, q8, rows, cols):
         out = np.empty(rows * cols // 32 * 34, np.uint8)

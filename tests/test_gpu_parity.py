@@ -323,6 +323,56 @@ def test_round_one_launch_equals_singles(rt, oracle, t):
             rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+def test_row_read_and_gather(rt, oracle):
+    """rt_q8_row (the embedding read, the reference's signature) and rt_q8_rows_dev (a batch of rows)
+    give the oracle's d * q bit for bit, including subnormal and zero scales."""
+    rows, cols = 256, 2048
+    q8, _ = synth.case(71, rows, cols, 1, "lognormal")
+    q, d = synth.split(q8, rows, cols)
+    d[3, :4] = 0
+    d[5, 4:9] = np.uint16(3).view(np.float16)
+    q8 = synth.join(q, d)
+    w = rt.upload(q8, rows, cols)
+    try:
+        for r in (0, 3, 5, 17, 255):
+            z = np.empty(cols, np.float32)
+            rt.lib.rt_q8_row(c.c_void_p(w), cols, r, z.ctypes.data_as(c.c_void_p))
+            assert np.array_equal(z.view(np.uint32), oracle.row(q8, cols, r).view(np.uint32)), r
+        idx = np.array([7, 0, 255, 7, 128], np.int64)
+        with Dev(rt) as dv:
+            pi, pz = dv.put(idx), dv.empty(4 * cols * idx.size)
+            rt.lib.rt_q8_rows_dev(rt.R, c.c_void_p(w), cols, c.c_void_p(pi), idx.size, c.c_void_p(pz))
+            z = dv.get(pz, (idx.size, cols), np.float32)
+        for k, r in enumerate(idx):
+            assert np.array_equal(z[k].view(np.uint32), oracle.row(q8, cols, int(r)).view(np.uint32))
+    finally:
+        rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
+def test_next_token_on_device(rt, oracle):
+    """rt_argmax_dev equals the oracle's rt_maxv + rt_index_of restatement: the 9B vocabulary
+    (151936 logits), ragged sizes around the 4096-element chunks, ties and NaN entries."""
+    rng = np.random.default_rng(19)
+    cases = []
+    for n in (1, 17, 4095, 4096, 4097, 12289, 151936):
+        a = (rng.standard_normal(n) * 4).astype(np.float32)
+        cases.append(a)
+        t = a.copy()
+        t[rng.integers(0, n, 3)] = t.max() + 1
+        cases.append(t)
+        if n > 2:
+            u = a.copy()
+            u[rng.integers(0, n, max(1, n // 7))] = np.nan
+            cases.append(u)
+    with Dev(rt) as dv:
+        out = dv.empty(8)
+        for a in cases:
+            pa = dv.put(a)
+            rt.lib.rt_argmax_dev(rt.R, c.c_void_p(pa), a.size, c.c_void_p(out))
+            got = int(dv.get(out, 1, np.int64)[0])
+            assert got == oracle.next(a), (a.size, got, oracle.next(a))
+
+
 def test_exact_kernels_at_config_shapes(rt, oracle):
     """Bit-identical to the oracle (the reference's order) at the 9B shapes, tokens 1 and 3."""
     for rows, cols, t in [(4096, 12288, 1), (6144, 4096, 3)]:

@@ -178,3 +178,47 @@ def test_planted_mistakes_are_caught(oracle):
     assert fails((qf * np.roll(df, 32, axis=1)) @ xf)
     assert fails((qf * df)[:, ::-1] @ xf)
     assert fails((-qf * df) @ xf)
+
+
+def _logits(rng, n):
+    return rng.standard_normal(n).astype(np.float32) * 4
+
+
+def test_next_token_matches_reference(oracle, reference):
+    """q8o_next against the reference's rt_maxv + rt_index_of, and numpy: ragged lengths, ties (the
+    lowest index wins), NaN entries (fmaxf skips them), all-negative and constant arrays."""
+    if reference is None:
+        pytest.skip("the reference's sources are not here to build oracle/_ref")
+    rng = np.random.default_rng(11)
+    cases = []
+    for n in (1, 2, 15, 16, 17, 31, 1000, 4096, 4097, 151936):
+        a = _logits(rng, n)
+        cases.append(a)
+        t = a.copy()
+        j = rng.integers(0, n, 3)
+        t[j] = t.max() + 1.0  # a three-way tie at the top
+        cases.append(t)
+        if n > 2:
+            u = a.copy()
+            u[rng.integers(0, n, max(1, n // 10))] = np.nan
+            u[0] = np.nan
+            cases.append(u)
+    cases += [np.full(33, -3.0, np.float32), -np.abs(_logits(rng, 100)) - 1]
+    for a in cases:
+        got = oracle.next(a)
+        assert got == reference.next(a), (a.size, got, reference.next(a))
+        if not np.isnan(a).all():
+            assert got == int(np.nanargmax(a))
+
+
+def test_row_read_matches_reference(oracle, reference):
+    """q8o_row equals the reference's rt_q8_row on form I bit for bit, and numpy's d * q (exact)."""
+    rows, cols = 64, 512
+    q8, _ = synth.case(44, rows, cols, 1, "lognormal")
+    q, d = synth.split(q8, rows, cols)
+    for r in (0, 1, 15, 16, 37, 63):
+        got = oracle.row(q8, cols, r)
+        want = np.repeat(d[r].astype(np.float32), 32) * q[r].astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        if reference is not None:
+            assert np.array_equal(got.view(np.uint32), reference.row(q8, rows, cols, r).view(np.uint32))
