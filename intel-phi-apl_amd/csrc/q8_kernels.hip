@@ -300,6 +300,10 @@ static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, lo
     int rw = PAIR ? 4 : 8, nw = kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
+    /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
+     * SIMD) stream */
+    while (rw > 2 && rows / rw * nw < 2048)
+        rw /= 2;
     int erw, enw;
     if (gemv_env(&erw, &enw))
         rw = erw, nw = enw;
