@@ -294,6 +294,47 @@ def deltanet_round(b):
     return out
 
 
+def host_pointers(b):
+    """The reference's entry points with host arrays (x copied in, y copied back, one wait a call):
+    rt_gemv on 4096x4096 and the 9B DeltaNet quartet queued with rt_gemv_q and run by rt_gemv_go,
+    over rotated weights. The PCIe-inclusive rate, reported beside the HBM-resident one."""
+    out = {}
+    x = np.random.default_rng(3).standard_normal(HIDDEN, dtype=np.float32)
+    ws = rotation(b, 4096, 4096)
+    y = np.empty(4096, np.float32)
+    b.rt.gemv(ws[0], 4096, 4096, x, y)
+    t0 = time.perf_counter()
+    reps = 5
+    for _ in range(reps):
+        for w in ws:
+            b.rt.gemv(w, 4096, 4096, x, y)
+    us = (time.perf_counter() - t0) / (reps * len(ws)) * 1e6
+    out["rt_gemv_4096x4096"] = {"us_per_call": round(us, 2), "GB/s": round(alg_bytes(4096, 4096, 1) / us / 1e3, 1)}
+    for w in ws:
+        b.rt.free(w)
+    shapes = [8192, 4096, 32, 32]
+    quartets = [[b.matrix(r, HIDDEN) for r in shapes] for _ in range(12)]
+    ys = [np.empty(r, np.float32) for r in shapes]
+    per = sum(alg_bytes(r, HIDDEN, 1) for r in shapes) - 3 * 4 * HIDDEN
+
+    def round_(Q):
+        b.rt.gemv_open()
+        for w, r, yy in zip(Q, shapes, ys):
+            b.rt.gemv_q(w, r, HIDDEN, x, yy)
+        b.rt.gemv_go()
+    round_(quartets[0])
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for Q in quartets:
+            round_(Q)
+    us = (time.perf_counter() - t0) / (reps * len(quartets)) * 1e6
+    out["quartet_round_9b"] = {"us_per_round": round(us, 2), "GB/s": round(per / us / 1e3, 1)}
+    for Q in quartets:
+        for w in Q:
+            b.rt.free(w)
+    return out
+
+
 def layers_2b(b):
     """Config 2: 24 layers of QKV 3072x2048, out 2048x2048, gate/up 6144x2048 (fused), down 2048x6144."""
     H, F, Q = 2048, 6144, 2048 + 2 * 512
@@ -512,7 +553,7 @@ def main():
     name, cus = b.rt.device_info()
     log(f"device: {name}, {cus} CUs")
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
-                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round))
+                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers))
     if a.only:
         want = a.only.split(",")
         for key, fn in sections:
