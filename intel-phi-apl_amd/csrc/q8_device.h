@@ -129,14 +129,10 @@ struct q8_round {
 int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
 /* The reference's order, every y bit-identical to the reference's F32 host path. */
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
-/* Y = X W^T for 5 <= t <= 64 on the matrix cores: the x limb pass, then the product. xs holds
- * q8_gemm_xs_bytes(cols, t) bytes, part q8_gemm_part_floats(rows, cols, t) floats (at most
- * Q8_GEMM_PART_MAX), counters Q8_GEMM_COUNTERS words that are zero, and are zero again after. */
+/* Y = X W^T for 5 <= t <= 64 on the matrix cores (and the sum of the K split's partials). part
+ * holds q8_gemm_part_floats(rows, cols, t) floats, at most Q8_GEMM_PART_MAX. */
 #define Q8_GEMM_PART_MAX (8L << 20)
-#define Q8_GEMM_COUNTERS 1024
-void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, void *xs, float *part,
-                         uint32_t *counters);
-long q8_gemm_xs_bytes(long cols, long t);
+void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part);
 long q8_gemm_part_floats(long rows, long cols, long t);
 /* the kernel's choice for a shape: MG token tiles, RT row tiles a wave, KP pairs of blocks and NW
  * waves a workgroup, ks workgroups along K, cps ranges of KP pairs a workgroup */

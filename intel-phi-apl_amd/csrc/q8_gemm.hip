@@ -11,21 +11,16 @@
  * hi*q + mid*q + lo*q see every bit of x; each product is exact and the matrix core adds them
  * in F32. Accuracy is that of an F32 sum, far inside NRMSE 1e-5.
  *
- * Layouts (lane l of a wave): A = x limbs, A[m][k] at lane m + 16*(k/8), item k%8 (m = token);
- * B = weights, B[k][n] at lane n + 16*(k/8), item k%8 (n = row of W: 8 bytes of row n of form
- * S, one global_load_dwordx2); D[m][n] at lane n + 16*(m/4), item m%4. So each lane needs the
- * scale of one row per block, and x_split's A tiles are 1 KiB each, read whole by a wave.
+ * Layouts (lane l of a wave): A = x limbs, A[m][k] at lane m + 16*(k/8) (m = token); B = weights,
+ * B[k][n] at lane n + 16*(k/8) (n = row of W); D[m][n] at lane n + 16*(m/4), item m%4. So each
+ * lane needs the scale of one row per block. Within a block the lane groups hold the columns
+ * KCOL(kq) .. +7 (below), in both operands.
  *
- *   xsplit      x F32 [t cols] -> the limbs in A layout, tokens padded to 16 with zeros:
- *               xs[((tt*nb + b)*3 + limb)*64 + lane] = 8 bf16 (one uint4)
- *   gemm_mfma   a workgroup of 4 waves owns 4*RT row tiles of 16 rows (waves split rows, so the
- *               four read the same x tiles: one L2 read, three L1 hits) and a range of blocks;
- *               with the blocks split over KS workgroups, each writes its partial Y to a
- *               workspace with device-scope stores, and the last of the KS to finish (a
- *               counter per row tile, atomically incremented once the workgroup's stores are
- *               acknowledged) reads the KS partials with device-scope loads, adds them in
- *               split order and writes Y. The same order every run: deterministic. The last
- *               one also resets the counter, so the counters stay zero between products. */
+ *   gemm_mfma   a workgroup of NW waves owns NW row tiles of 16 rows and KP pairs of blocks; it
+ *               loads the range's x (split into limbs on the way into LDS), its rows' scales (into
+ *               LDS) and every weight of every wave at once, then runs the MFMAs. With the K range
+ *               split over ks workgroups, each writes a partial;
+ *   gemm_sum    adds the ks partials in split order: the same order every run, deterministic. */
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
@@ -50,30 +45,12 @@ __device__ __forceinline__ uint32_t pack_hi(float a, float b)
  * over the block's 32 columns exactly once. */
 __host__ __device__ constexpr int kcol(int kq) { return 8 * ((kq & 1) * 2 + (kq >> 1)); }
 
-/* ---------------------------------------------------------------- x -> bf16 limbs */
-
-/* xs[((tt*nbp + b)*3 + limb)*64 + lane], nbp = nb rounded up to even (the odd block's partner is
- * zeros), tokens padded to 16 with zeros */
-__global__ __launch_bounds__(256) void xsplit(const float *__restrict__ x, long x_stride, long t, long cols, long mt, uint4 *__restrict__ xs)
+/* 8 F32 values to their three bf16 limbs (8 each): hi = the top 16 bits, r = x - hi exactly,
+ * mid = r's top 16 bits, lo = r - mid exactly (at most 8 significant bits) */
+__device__ __forceinline__ void xsplit8(float4 a, float4 c, uint4 &h, uint4 &m, uint4 &o)
 {
-    const long nb = cols / Q8_BLOCK, nbp = (nb + 1) & ~1L;
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= mt * nbp * 64)
-        return;
-    const int lane = (int)(i & 63);
-    const long b = (i >> 6) % nbp, tt = (i >> 6) / nbp;
-    const long tok = tt * 16 + (lane & 15);
-    const long k0 = b * Q8_BLOCK + kcol(lane >> 4);
-    float v[8];
-    if (tok < t && b < nb) {
-        const float4 a = *(const float4 *)(x + tok * x_stride + k0), c = *(const float4 *)(x + tok * x_stride + k0 + 4);
-        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = c.x, v[5] = c.y, v[6] = c.z, v[7] = c.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            v[j] = 0.0f;
-    }
-    uint32_t h[4], m[4], o[4];
+    const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+    uint32_t hh[4], mm[4], oo[4];
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
         float hi[2], mid[2], lo[2];
@@ -84,14 +61,13 @@ __global__ __launch_bounds__(256) void xsplit(const float *__restrict__ x, long 
             mid[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, r) & 0xffff0000u);
             lo[e] = r - mid[e];
         }
-        h[j / 2] = pack_hi(hi[0], hi[1]);
-        m[j / 2] = pack_hi(mid[0], mid[1]);
-        o[j / 2] = pack_hi(lo[0], lo[1]);
+        hh[j / 2] = pack_hi(hi[0], hi[1]);
+        mm[j / 2] = pack_hi(mid[0], mid[1]);
+        oo[j / 2] = pack_hi(lo[0], lo[1]);
     }
-    uint4 *dst = xs + ((tt * nbp + b) * 3) * 64 + lane;
-    dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
-    dst[64] = make_uint4(m[0], m[1], m[2], m[3]);
-    dst[128] = make_uint4(o[0], o[1], o[2], o[3]);
+    h = make_uint4(hh[0], hh[1], hh[2], hh[3]);
+    m = make_uint4(mm[0], mm[1], mm[2], mm[3]);
+    o = make_uint4(oo[0], oo[1], oo[2], oo[3]);
 }
 
 /* ---------------------------------------------------------------- the product */
@@ -132,104 +108,20 @@ __device__ __forceinline__ void load_x(uint4 (&xa)[MT][3], const uint4 *xs, long
             xa[m][l] = xs[((m * nbp + b) * 3 + l) * 64 + lane];
 }
 
-/* Y (ks == 1) or this split's partial (ks > 1) from the accumulators of the waves that write, for
- * token tiles [tt0/16.., +MT); with ks > 1 the last workgroup of a row range (counter cnt) sums the
- * splits. rows_wg: the workgroup's rows, from row tile*rows_wg. Partials: part[split][token][row]
- * over all the product's padded tokens, so token groups of one row range share nothing. */
-template <int MT, int RT>
-__device__ __forceinline__ void gemm_out(const f32x4 (&acc)[RT][MT], bool writer, long rt0, long rows, long t, long tt0, int ks, int split, long cnt,
-                                         long tile, long rows_wg, float *__restrict__ part, uint32_t *__restrict__ counters, float *__restrict__ y)
-{
-    const int lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
-    /* lane holds D[token 16m + 4*kq + j][row 16*(rt0+r) + n] */
-    if (ks == 1) {
-        if (!writer)
-            return;
-#pragma unroll
-        for (int r = 0; r < RT; r++)
-#pragma unroll
-            for (int m = 0; m < MT; m++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const long tok = 16 * (tt0 + m) + 4 * kq + j;
-                    if (tok < t)
-                        y[tok * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
-                }
-        return;
-    }
-    /* split K: part[split][token (16*MT)][rows]. The partials go out as device-scope stores (sc1:
-     * through this XCD's L2 to where every XCD reads), every lane waits for its own to be
-     * acknowledged, and only then does the workgroup count itself in; the last one in reads
-     * them as device-scope loads. No whole-L2 write-back or invalidate (an agent-scope fence)
-     * is needed, and none is made: hundreds of workgroups serialise on those. */
-    const long tp = (t + 15) / 16 * 16;
-#pragma unroll
-    for (int r = 0; r < (writer ? RT : 0); r++)
-#pragma unroll
-        for (int m = 0; m < MT; m++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (16 * (tt0 + m) < tp) /* a group's tile past the last holds no tokens */
-                    __hip_atomic_store(&part[((long)split * tp + 16 * (tt0 + m) + 4 * kq + j) * rows + (rt0 + r) * 16 + n], acc[r][m][j], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    __shared__ uint32_t last;
-    __builtin_amdgcn_s_waitcnt(0); /* this lane's stores acknowledged */
-    __syncthreads();
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(&counters[cnt], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(ks - 1);
-    __syncthreads();
-    if (!last)
-        return;
-    /* the last workgroup: its rows x its tokens, summed in split order */
-    const long r0 = tile * rows_wg;
-    const long nr = rows - r0 < rows_wg ? rows - r0 : rows_wg;
-    const long tok0 = 16 * tt0, nt = t - tok0 < 16 * MT ? t - tok0 : 16 * MT;
-    const long n_out = nt * nr;
-    /* four outputs a thread at a time, every split's load of them issued before the sums */
-    for (long i0 = threadIdx.x; i0 < n_out; i0 += 4 * (long)blockDim.x) {
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < ks; s0 += 8) {
-            float ld[8][4];
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const long i = i0 + e * (long)blockDim.x;
-                    const long tok = tok0 + i / nr, row = r0 + i % nr;
-                    ld[s][e] = s0 + s < ks && i < n_out
-                                   ? __hip_atomic_load(&part[((long)(s0 + s) * tp + tok) * rows + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                   : 0.0f;
-                }
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    v[e] = s0 + s == 0 ? ld[s][e] : s0 + s < ks ? v[e] + ld[s][e] : v[e];
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const long i = i0 + e * (long)blockDim.x;
-            if (i < n_out)
-                y[(tok0 + i / nr) * rows + r0 + i % nr] = v[e];
-        }
-    }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(&counters[cnt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 /* A workgroup of NW waves owns NW*RT row tiles of 16 rows (wave w: tiles [w*RT, +RT)), KP pairs
  * of blocks (split s: pairs [s*KP, +KP)) and MT token tiles (from token tile tt0 = blockIdx.y*MT).
  * Like the decode kernel, everything is issued at once: the x limbs of the range, then every
  * weight of the wave (KP pairs x RT row tiles, 16 B a lane); a memory-bound kernel is as fast as
  * the bytes it keeps in flight. The x limbs go to LDS once for the workgroup (x is issued first:
  * loads retire in order, so the LDS write waits for x only) and the NW waves read them there.
- * The ks workgroups of a row range are summed by the last to finish (gemm_out). */
+ * The ks workgroups of a row range write partials that gemm_sum adds in split order. */
 template <int MT, int RT, int KP, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__ w, long rows, long cols, const uint4 *__restrict__ xs, long t, int ks,
-                                                     int cps, float *__restrict__ part, uint32_t *__restrict__ counters, float *__restrict__ y)
+__global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__ w, long rows, long cols, const float *__restrict__ x, long x_stride,
+                                                     long t, int ks, int cps, float *__restrict__ part, float *__restrict__ y)
 {
     constexpr int XN = MT * 2 * KP * 192;              /* uint4 of x limbs in the range */
-    constexpr int XR = (XN + 64 * NW - 1) / (64 * NW); /* of them a thread */
+    constexpr int XS = MT * 2 * KP * 64;               /* lane slots: 8 x values, three limbs each */
+    constexpr int XR = (XS + 64 * NW - 1) / (64 * NW); /* of them a thread */
     constexpr int DN = NW * RT * 16 * 2 * KP;          /* scales of the workgroup's rows in the range */
     constexpr int DR = (DN + 64 * NW - 1) / (64 * NW);
     __shared__ uint4 xl[XN];                           /* [tt][block in range][limb][lane] */
@@ -253,16 +145,21 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
     /* cps ranges of KP pairs a workgroup (one unless the K split would not fit its workspace) */
     for (int ch = 0; ch < cps; ch++) {
         const long c0 = ((long)split * cps + ch) * KP;
-        /* x limbs of blocks [2*c0, 2*c0 + 2*KP) for token tiles [tt0, tt0 + MT), clamped to the matrix */
-        uint4 xr[XR];
+        /* x of blocks [2*c0, 2*c0 + 2*KP) for token tiles [tt0, tt0 + MT): a lane slot is 8 values of
+         * one token (zeros past t or past the last block), split into its three limbs here */
+        float4 xr[XR][2];
 #pragma unroll
         for (int k = 0; k < XR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
-            if (XN % (64 * NW) == 0 || i < XN) {
-                const int tt = i / (2 * KP * 192), rem = i % (2 * KP * 192);
-                long b = 2 * c0 + rem / 192;
-                b = b < nbp ? b : nbp - 1;
-                xr[k] = xs[((tt0 + tt) * nbp + b) * 192 + rem % 192];
+            xr[k][0] = xr[k][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (XS % (64 * NW) == 0 || i < XS) {
+                const int L = i & 63, bb = (i >> 6) % (2 * KP), tt = (i >> 6) / (2 * KP);
+                const long tok = 16 * (tt0 + tt) + (L & 15), b = 2 * c0 + bb;
+                if (tok < t && b < nb) {
+                    const float *px = x + tok * x_stride + b * Q8_BLOCK + kcol(L >> 4);
+                    xr[k][0] = *(const float4 *)px;
+                    xr[k][1] = *(const float4 *)(px + 4);
+                }
             }
         }
         /* the scales of the workgroup's rows for the range: 2*KP consecutive threads read one row's
@@ -292,8 +189,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
 #pragma unroll
         for (int k = 0; k < XR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
-            if (XN % (64 * NW) == 0 || i < XN)
-                xl[i] = xr[k];
+            if (XS % (64 * NW) == 0 || i < XS) {
+                const int L = i & 63, blk = i >> 6; /* blk = tt * 2KP + bb */
+                uint4 h, m, o;
+                xsplit8(xr[k][0], xr[k][1], h, m, o);
+                xl[(blk * 3 + 0) * 64 + L] = h;
+                xl[(blk * 3 + 1) * 64 + L] = m;
+                xl[(blk * 3 + 2) * 64 + L] = o;
+            }
         }
 #pragma unroll
         for (int k = 0; k < DR; k++) {
@@ -335,16 +238,41 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
         }
         __syncthreads(); /* every wave done with xl before the next range overwrites it */
     }
-    gemm_out<MT, RT>(acc, live, rt0, rows, t, tt0, ks, split, tile + (long)blockIdx.y * gridDim.x / ks, tile, 16L * NW * RT, part, counters, y);
+    /* lane holds D[token 16(tt0+m) + 4*kq + j][row 16*(rt0+r) + n]: to Y, or to this split's
+     * partial, part[split][token][row] over the product's padded tokens (summed by gemm_sum) */
+    if (!live)
+        return;
+    const long tp = (t + 15) / 16 * 16;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const long tok = 16 * (tt0 + m) + 4 * kq + j;
+                if (ks == 1) {
+                    if (tok < t)
+                        y[tok * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
+                } else if (tok < tp) {
+                    part[((long)split * tp + tok) * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
+                }
+            }
+}
+
+/* Y = the sum of the ks partials in split order, one thread an output (the kernel boundary
+ * before it makes every split's stores visible) */
+__global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *__restrict__ y)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= t * rows)
+        return;
+    float v = part[i];
+    for (int s = 1; s < ks; s++)
+        v += part[(long)s * tp * rows + i];
+    y[i] = v;
 }
 
 /* ---------------------------------------------------------------- launchers */
-
-long q8_gemm_xs_bytes(long cols, long t)
-{
-    const long nb = cols / Q8_BLOCK;
-    return ((t + 15) / 16 + 1) * ((nb + 1) & ~1L) * 3 * 1024; /* one spare token tile: groups of 2 */
-}
 
 /* The instantiated configurations: MG token tiles a workgroup (the product's MT token tiles in
  * groups of MG, over blockIdx.y), RT row tiles a wave, KP pairs a workgroup, NW waves a workgroup.
@@ -373,8 +301,9 @@ static bool env_cfg(gemm_cfg *c)
 void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *nw, int *ks, int *cps)
 {
     const long mt = (t + 15) / 16, rt16 = rows / 16;
-    /* measured on the 9B FFN matrices: 16-pair ranges for one token tile, 4-pair ranges beyond */
-    gemm_cfg c = mt == 1 ? CFGS[5] : CFGS[4];
+    /* measured on the 9B FFN matrices: 4-pair ranges and 8 waves; two token tiles a workgroup
+     * from 17 tokens on */
+    gemm_cfg c = mt == 1 ? CFGS[4] : CFGS[6];
     gemm_cfg e;
     if (env_cfg(&e) && e.mg <= mt)
         c = e;
@@ -384,10 +313,11 @@ void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
     const long groups = (mt + c.mg - 1) / c.mg;
     const long ranges = (np + c.kp - 1) / c.kp;
-    /* ranges a workgroup: one, unless the partials or the counters would not fit */
+    /* ranges a workgroup: one, unless the partials would not fit the workspace */
     long per = 1;
-    while (per < ranges && ((ranges + per - 1) / per * mt * 16 * rows > Q8_GEMM_PART_MAX || tiles * groups > Q8_GEMM_COUNTERS))
+    while (per < ranges && (ranges + per - 1) / per * mt * 16 * rows > Q8_GEMM_PART_MAX)
         per++;
+    (void)tiles, (void)groups;
     *mg = c.mg, *rt = c.rt, *kp = c.kp, *nw = c.nw, *cps = (int)per;
     *ks = (int)((ranges + per - 1) / per);
 }
@@ -400,29 +330,25 @@ long q8_gemm_part_floats(long rows, long cols, long t)
 }
 
 template <int MG, int RT, int KP, int NW>
-static void gemm_go(hipStream_t s, const void *w, long rows, long cols, long t, float *y, void *xs, float *part, uint32_t *counters, int ks, int cps)
+static void gemm_go(hipStream_t s, const void *w, long rows, long cols, const float *x, long xst, long t, float *y, float *part, int ks, int cps)
 {
     const long tiles = (rows + 16L * NW * RT - 1) / (16L * NW * RT);
     const long groups = ((t + 15) / 16 + MG - 1) / MG;
     Q8_LAUNCH(q8_time_name("gemm_mfma", 4, MG, RT, KP, NW), (gemm_mfma<MG, RT, KP, NW>), dim3((unsigned)(tiles * ks), (unsigned)groups),
-              dim3(64 * NW), s, (const uint8_t *)w, rows, cols, (const uint4 *)xs, t, ks, cps, part, counters, y);
+              dim3(64 * NW), s, (const uint8_t *)w, rows, cols, x, xst, t, ks, cps, part, y);
 }
 
-void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, void *xs, float *part,
-                         uint32_t *counters)
+void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part)
 {
     hipStream_t s = (hipStream_t)stream;
     int mg, rt, kp, nw, ks, cps;
     q8_gemm_plan(rows, cols, t, &mg, &rt, &kp, &nw, &ks, &cps);
-    const long mt = (t + 15) / 16;
-    /* token tiles past t hold zeros; a group's last tile may lie past mt (groups of MG): the
-     * limbs are laid out for whole groups */
-    const long mtp = (mt + mg - 1) / mg * mg;
-    const long n = mtp * (((cols / Q8_BLOCK) + 1) & ~1L) * 64;
-    xsplit<<<dim3((unsigned)((n + 255) / 256)), 256, 0, s>>>(x, x_stride, t, cols, mtp, (uint4 *)xs);
+    float *out = ks > 1 ? part : y;
 #define GO(G, R, P, N)                                                                                                 \
     if (mg == G && rt == R && kp == P && nw == N) {                                                                    \
-        gemm_go<G, R, P, N>(s, w, rows, cols, t, y, xs, part, counters, ks, cps);                                      \
+        gemm_go<G, R, P, N>(s, w, rows, cols, x, x_stride, t, out, part, ks, cps);                                      \
+        if (ks > 1)                                                                                                    \
+            gemm_sum<<<dim3((unsigned)((t * rows + 255) / 256)), 256, 0, s>>>(part, ks, t, (t + 15) / 16 * 16, rows, y); \
         return;                                                                                                        \
     }
     GO(1, 1, 8, 8) GO(1, 2, 8, 4) GO(1, 1, 8, 4) GO(1, 2, 4, 8) GO(1, 1, 4, 8) GO(1, 1, 16, 8) GO(2, 1, 4, 8) GO(2, 1, 8, 4) GO(2, 2, 4, 4)

@@ -63,11 +63,8 @@ struct ctx {
     /* scratch for the fused pair when it runs as two products (exact mode, t >= 5): G and U */
     float *scratch = nullptr;
     size_t scratch_cap = 0;
-    /* the matrix-core product's workspace: x limbs, K-split partials, per-tile counters */
-    void *xs = nullptr;
-    size_t xs_cap = 0;
+    /* the matrix-core product's K-split partials */
     float *part = nullptr;
-    uint32_t *counters = nullptr;
     /* the greedy next token's candidates */
     void *amax = nullptr;
     size_t amax_cap = 0;
@@ -173,19 +170,9 @@ float *reserve_scratch(ctx *c, size_t n)
 
 void reserve_gemm(ctx *c, long rows, long cols, long t)
 {
-    const size_t xb = (size_t)q8_gemm_xs_bytes(cols, t);
-    if (xb > c->xs_cap) {
-        no_capture(c, "the matrix-core product's x workspace");
-        if (c->xs)
-            c->retired.push_back(c->xs);
-        HIPCHECK(hipMalloc(&c->xs, xb));
-        c->xs_cap = xb;
-    }
     if (!c->part && q8_gemm_part_floats(rows, cols, t) > 0) {
         no_capture(c, "the matrix-core product's partial sums");
         HIPCHECK(hipMalloc((void **)&c->part, (size_t)Q8_GEMM_PART_MAX * sizeof(float)));
-        HIPCHECK(hipMalloc((void **)&c->counters, Q8_GEMM_COUNTERS * sizeof(uint32_t)));
-        HIPCHECK(hipMemsetAsync(c->counters, 0, Q8_GEMM_COUNTERS * sizeof(uint32_t), c->stream));
     }
     if (q8_gemm_part_floats(rows, cols, t) > Q8_GEMM_PART_MAX)
         fail("the matrix-core product", "its K-split partials exceed the workspace (a planning error)");
@@ -201,7 +188,7 @@ void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, lo
             continue;
         }
         reserve_gemm(c, rows, cols, n);
-        q8_launch_gemm_mfma((q8_stream_t)c->stream, w, rows, cols, x + k * xs, xs, n, y + k * rows, c->xs, c->part, c->counters);
+        q8_launch_gemm_mfma((q8_stream_t)c->stream, w, rows, cols, x + k * xs, xs, n, y + k * rows, c->part);
     }
 }
 
@@ -386,12 +373,8 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipFree(c->dy));
     if (c->scratch)
         HIPCHECK(hipFree(c->scratch));
-    if (c->xs)
-        HIPCHECK(hipFree(c->xs));
     if (c->part)
         HIPCHECK(hipFree(c->part));
-    if (c->counters)
-        HIPCHECK(hipFree(c->counters));
     for (void *p : c->retired)
         HIPCHECK(hipFree(p));
     for (auto &e : c->kt_events)
