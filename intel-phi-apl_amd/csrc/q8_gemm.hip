@@ -266,9 +266,21 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= t * rows)
         return;
+    const long step = tp * rows;
+    /* eight splits' loads in flight at a time, added in split order */
     float v = part[i];
-    for (int s = 1; s < ks; s++)
-        v += part[(long)s * tp * rows + i];
+    int s = 1;
+    for (; s + 8 <= ks; s += 8) {
+        float a[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            a[k] = part[(long)(s + k) * step + i];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            v += a[k];
+    }
+    for (; s < ks; s++)
+        v += part[(long)s * step + i];
     y[i] = v;
 }
 
@@ -280,7 +292,8 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
 struct gemm_cfg {
     int mg, rt, kp, nw;
 };
-static const gemm_cfg CFGS[] = {{1, 1, 8, 8}, {1, 2, 8, 4}, {1, 1, 8, 4}, {1, 2, 4, 8}, {1, 1, 4, 8}, {1, 1, 16, 8}, {2, 1, 4, 8}, {2, 1, 8, 4}, {2, 2, 4, 4}};
+static const gemm_cfg CFGS[] = {{1, 1, 8, 8}, {1, 2, 8, 4}, {1, 1, 8, 4}, {1, 2, 4, 8}, {1, 1, 4, 8}, {1, 1, 16, 8}, {2, 1, 4, 8}, {2, 1, 8, 4}, {2, 2, 4, 4},
+                                {1, 1, 4, 16}, {2, 1, 4, 16}, {1, 1, 2, 16}, {2, 1, 2, 8}};
 #define NCFG ((int)(sizeof(CFGS) / sizeof(CFGS[0])))
 
 /* Q8_GEMM_CFG = "MG,RT,KP,NW" picks an instantiated configuration, for tuning sweeps. */
@@ -352,6 +365,7 @@ void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols
         return;                                                                                                        \
     }
     GO(1, 1, 8, 8) GO(1, 2, 8, 4) GO(1, 1, 8, 4) GO(1, 2, 4, 8) GO(1, 1, 4, 8) GO(1, 1, 16, 8) GO(2, 1, 4, 8) GO(2, 1, 8, 4) GO(2, 2, 4, 4)
+    GO(1, 1, 4, 16) GO(2, 1, 4, 16) GO(1, 1, 2, 16) GO(2, 1, 2, 8)
 #undef GO
     fprintf(stderr, "q8_gemm: no kernel for MG %d RT %d KP %d NW %d\n", mg, rt, kp, nw);
     abort();
