@@ -506,6 +506,70 @@ def summarize(run_dir, out=DECODE_PROFILE):
     print(f"wrote {out}")
 
 
+GEMM_PROFILE = os.path.join(PROFILES, "gemm_prompt_9b_ffn.md")
+GEMM_PROFILE_CMDS = [
+    "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/gprof_stats -o run -- python3 bench.py --only prompt_gemm "
+    "> gpurun_out/gprof_stats.log 2>&1",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/gprof_fetch -o run -- python3 bench.py --only prompt_gemm",
+    "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv "
+    "-d gpurun_out/gprof_mfma -o run -- python3 bench.py --only prompt_gemm",
+    "python3 bench.py --summarize-gemm gpurun_out",
+]
+
+
+def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
+    """profiles/gemm_prompt_9b_ffn.md from the three rocprofv3 runs of GEMM_PROFILE_CMDS: per GEMM
+    kernel and grid, its mean duration (kernel trace), HBM bytes (FETCH_SIZE, scaled as for the
+    decode profile: x2.0), and MFMA utilisation = SQ_VALU_MFMA_BUSY_CYCLES over (GRBM_GUI_ACTIVE per
+    XCD x SIMDs), with the bf16 MFMA ops the counters saw (512 flop a MOP) against the issued work."""
+    import csv
+    from collections import defaultdict
+
+    line = json.loads(next(l for l in open(os.path.join(run_dir, "gprof_stats.log")) if l.startswith('{"prompt_gemm"')))["prompt_gemm"]
+    trace = defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(run_dir, "gprof_stats", "run_kernel_trace.csv"))):
+        g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        trace[(_kname(r["Kernel_Name"]), g)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    cnt = defaultdict(lambda: defaultdict(list))
+    for sub in ("gprof_fetch", "gprof_mfma"):
+        for r in csv.DictReader(open(os.path.join(run_dir, sub, "run_counter_collection.csv"))):
+            cnt[(_kname(r["Kernel_Name"]), int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    mean = lambda v: statistics.fmean(v) if v else float("nan")  # noqa: E731
+    rows = []
+    for shape, k in line.items():
+        m = int(shape.split()[0][1:])
+        r_, c_ = (int(v) for v in shape.split()[1].split("x"))
+        name = k["kernel"]
+        # the grid rocprof reports is x*y*z threads: match on the name, and on the grid where it is unique
+        keys = [key for key in cnt if key[0] == name]
+        key = next((kk for kk in keys if abs(mean(trace.get(kk, [])) - k["kernel_us"]) / k["kernel_us"] < 0.5), keys[0] if keys else None)
+        c = cnt.get(key, {})
+        busy, gui = mean(c.get("SQ_VALU_MFMA_BUSY_CYCLES", [])), mean(c.get("GRBM_GUI_ACTIVE", []))
+        mops = mean(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", []))
+        util = busy / (gui / xcds * simds) if gui == gui and gui > 0 else float("nan")
+        mg = int(name.split("<")[1].split(",")[0])
+        issued = 2.0 * 3 * (16 * mg * -(-(-(-m // 16)) // mg)) * r_ * c_  # the token tiles the kernel runs: whole groups of MG
+        tr = trace.get(key, [])
+        rows.append(f"| {shape} | `{name}` | {mean(tr):.2f} | {k['kernel_us']:.2f} | {k['product_us']:.2f} | {k['GFLOPS']:.0f} | "
+                    f"{2.0 * mean(c.get('FETCH_SIZE', [])) * 1024 / 1e6:.1f} | {alg_bytes(r_, c_, m) / 1e6:.1f} | {100 * util:.1f} | "
+                    f"{mops * 512 / issued:.3f} |")
+    text = ["# Prompt / verify GEMM on the matrix cores, 9B FFN shapes (rocprofv3)", "",
+            "Workload: Y = X W^T, X F32 [M x cols], W Q8_0 gate/up 12288x4096 and down 4096x12288, M = 16, 40, 64; each product over "
+            ">= 512 MB of rotated weight copies. The contraction runs as bf16 MFMA on three exact limbs of x (3x the flops of the "
+            "product, tokens padded to 16).", "",
+            "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + GEMM_PROFILE_CMDS + ["```", "",
+            "| Product | Kernel | Trace avg us | Bench kernel us | Bench product us (with the partial sum) | GFLOP/s (product) | "
+            "HBM MB (FETCH_SIZE x2) | Algorithmic MB | MFMA busy % | counted bf16 MFMA flop / issued |", "|---|---|---|---|---|---|---|---|---|---|"]
+    text += rows
+    text += ["", f"MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). Counted flop = "
+             "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512; issued = 2 x 3 limbs x the token tiles the kernel runs (whole groups of MG "
+             "tiles of 16: at M = 40, 4 tiles, one of them all padding) x rows x cols. Counters are per (kernel, grid): the "
+             "12288x4096 and 4096x12288 products launch the same grid of the same work (a workgroup: 128 rows x 256 "
+             "columns), and M = 40 and 64 the same grid, so their counter columns are the same averages.", ""]
+    open(out, "w").write("\n".join(text))
+    print(f"wrote {out}")
+
+
 def profiled_traffic(kname, grid, path=DECODE_PROFILE):
     """HBM bytes per launch of (kernel, grid) from the committed rocprofv3 summary, or None."""
     try:
@@ -539,11 +603,15 @@ def main():
                     "draft_head, prompt_gemm, verify, 2b_layer_set); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
+    ap.add_argument("--summarize-gemm", metavar="DIR", help="write the GEMM rocprofv3 summary under profiles/ from DIR and exit")
     ap.add_argument("--calib", action="store_true", help="also copy 1 GiB three times with the plain copy kernel (the yardstick "
                     "for the HBM byte counters of a rocprofv3 --pmc run)")
     a = ap.parse_args()
     if a.summarize:
         summarize(a.summarize)
+        return
+    if a.summarize_gemm:
+        summarize_gemm(a.summarize_gemm)
         return
     if a.gpus != 1:
         print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (every product runs on one MI355X; see DESIGN.md "
