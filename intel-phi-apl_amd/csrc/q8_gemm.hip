@@ -108,24 +108,39 @@ __device__ __forceinline__ void load_x(uint4 (&xa)[MT][3], const uint4 *xs, long
             xa[m][l] = xs[((m * nbp + b) * 3 + l) * 64 + lane];
 }
 
-/* A workgroup of NW waves owns NW*RT row tiles of 16 rows (wave w: tiles [w*RT, +RT)), KP pairs
- * of blocks (split s: pairs [s*KP, +KP)) and MT token tiles (from token tile tt0 = blockIdx.y*MT).
- * Like the decode kernel, everything is issued at once: the x limbs of the range, then every
- * weight of the wave (KP pairs x RT row tiles, 16 B a lane); a memory-bound kernel is as fast as
- * the bytes it keeps in flight. The x limbs go to LDS once for the workgroup (x is issued first:
- * loads retire in order, so the LDS write waits for x only) and the NW waves read them there.
- * The ks workgroups of a row range write partials that gemm_sum adds in split order. */
+/* ranges a workgroup streams without draining its loads (one unrolled pipeline) */
+#define GEMM_CHUNK 8
+
+/* The loads of one range of KP pairs, held in registers from issue to commit. */
 template <int MT, int RT, int KP, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__ w, long rows, long cols, const float *__restrict__ x, long x_stride,
-                                                     long t, int ks, int cps, float *__restrict__ part, float *__restrict__ y)
+struct gemm_stage {
+    static constexpr int XS = MT * 2 * KP * 64;               /* x lane slots: 8 values of one token each */
+    static constexpr int XR = (XS + 64 * NW - 1) / (64 * NW); /* of them a thread */
+    static constexpr int DN = NW * RT * 16 * 2 * KP;          /* scales of the workgroup's rows */
+    static constexpr int DR = (DN + 64 * NW - 1) / (64 * NW);
+    float4 xr[XR][2];
+    bool xin[XR];
+    uint16_t dr[DR];
+    uint4 q[KP][RT];
+};
+
+/* A workgroup of NW waves owns NW*RT row tiles of 16 rows (wave w: tiles [w*RT, +RT)), MT token
+ * tiles (from token tile tt0 = blockIdx.y*MT) and cps consecutive ranges of KP pairs of blocks
+ * (split s: ranges [s*cps, +cps)). For each range it loads x (split into limbs on its way into
+ * LDS, shared by the NW waves), its rows' scales (into LDS) and every weight of every wave, all
+ * issued at once: a memory-bound kernel is as fast as the bytes it keeps in flight. The ranges
+ * are software-pipelined: the loads of range ch+1 are issued into a second register set before
+ * the MFMAs of range ch, so a workgroup streams its K slice with one range always in flight.
+ * The ks workgroups of a row tile write partials that gemm_sum adds in split order. */
+template <int MT, int RT, int KP, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                                     float *part, float *y)
 {
-    constexpr int XN = MT * 2 * KP * 192;              /* uint4 of x limbs in the range */
-    constexpr int XS = MT * 2 * KP * 64;               /* lane slots: 8 x values, three limbs each */
-    constexpr int XR = (XS + 64 * NW - 1) / (64 * NW); /* of them a thread */
-    constexpr int DN = NW * RT * 16 * 2 * KP;          /* scales of the workgroup's rows in the range */
-    constexpr int DR = (DN + 64 * NW - 1) / (64 * NW);
-    __shared__ uint4 xl[XN];                           /* [tt][block in range][limb][lane] */
-    __shared__ uint16_t dl[DN];                        /* [row of the workgroup][block in range] */
+    typedef gemm_stage<MT, RT, KP, NW> stage;
+    constexpr int XS = stage::XS, XR = stage::XR, DN = stage::DN, DR = stage::DR;
+    constexpr int XN = MT * 2 * KP * 192; /* uint4 of x limbs in a range */
+    __shared__ uint4 xls[2][XN];          /* two ranges: [tt][block in range][limb][lane] */
+    __shared__ uint16_t dls[2][DN];       /* two ranges: [row of the workgroup][block in range] */
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long nb = cols / Q8_BLOCK, nbp = (nb + 1) & ~1L, np = nbp / 2;
     const long tile = blockIdx.x / ks;
@@ -136,35 +151,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
     const bool live = rt0 < rows / 16;
     const int n = lane & 15, kq = lane >> 4;
 
-    f32x4 acc[RT][MT];
-#pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-        for (int m = 0; m < MT; m++)
-            acc[r][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    /* cps ranges of KP pairs a workgroup (one unless the K split would not fit its workspace) */
-    for (int ch = 0; ch < cps; ch++) {
-        const long c0 = ((long)split * cps + ch) * KP;
-        /* x of blocks [2*c0, 2*c0 + 2*KP) for token tiles [tt0, tt0 + MT): a lane slot is 8 values of
-         * one token (zeros past t or past the last block), split into its three limbs here */
-        float4 xr[XR][2];
+    /* issue every load of the range starting at pair c0. All are unconditional, from indices
+     * clamped to the matrix; what lies past t, past the last block or past the last pair is zeroed
+     * after the loads (a load under a branch would make the wave wait for it before the next). */
+    auto issue = [&](stage &S, long c0) {
+        /* x of blocks [2*c0, 2*c0 + 2*KP) for token tiles [tt0, tt0 + MT) */
 #pragma unroll
         for (int k = 0; k < XR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
-            xr[k][0] = xr[k][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (XS % (64 * NW) == 0 || i < XS) {
-                const int L = i & 63, bb = (i >> 6) % (2 * KP), tt = (i >> 6) / (2 * KP);
-                const long tok = 16 * (tt0 + tt) + (L & 15), b = 2 * c0 + bb;
-                if (tok < t && b < nb) {
-                    const float *px = x + tok * x_stride + b * Q8_BLOCK + kcol(L >> 4);
-                    xr[k][0] = *(const float4 *)px;
-                    xr[k][1] = *(const float4 *)(px + 4);
-                }
-            }
+            const int L = i & 63, bb = (i >> 6) % (2 * KP), tt = (i >> 6) / (2 * KP);
+            const long tok = 16 * (tt0 + tt) + (L & 15), b = 2 * c0 + bb;
+            S.xin[k] = (XS % (64 * NW) == 0 || i < XS) && tok < t && b < nb;
+            const float *px = x + (tok < t ? tok : t - 1) * x_stride + (b < nb ? b : nb - 1) * Q8_BLOCK + kcol(L >> 4);
+            S.xr[k][0] = *(const float4 *)px;
+            S.xr[k][1] = *(const float4 *)(px + 4);
         }
-        /* the scales of the workgroup's rows for the range: 2*KP consecutive threads read one row's
-         * 2*KP consecutive binary16 (clamped to the matrix: a block past the end is zeroed below) */
-        uint16_t dr[DR];
+        /* the scales: 2*KP consecutive threads read one row's 2*KP consecutive binary16 */
 #pragma unroll
         for (int k = 0; k < DR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
@@ -173,26 +175,31 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
                 row = row < rows ? row : rows - 1;
                 long b = 2 * c0 + i % (2 * KP);
                 b = b < nb ? b : nb - 1;
-                dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
+                S.dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
             }
         }
-        uint4 q[KP][RT];
 #pragma unroll
         for (int p = 0; p < KP; p++) {
-            const long c = c0 + p < np ? c0 + p : np - 1; /* clamped: a pair past the end is zeroed below */
+            const long c = c0 + p < np ? c0 + p : np - 1;
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 const long row = live ? (rt0 + r) * 16 + n : n;
-                q[p][r] = *(const uint4 *)(w + q8s_row_q(row, cols) + 16 * kq + 64 * c);
+                S.q[p][r] = *(const uint4 *)(w + q8s_row_q(row, cols) + 16 * kq + 64 * c);
             }
         }
+    };
+    /* the range's x limbs and scales into LDS buffer bf */
+    auto commit = [&](const stage &S, int bf) {
+        uint4 *xl = xls[bf];
+        uint16_t *dl = dls[bf];
 #pragma unroll
         for (int k = 0; k < XR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
             if (XS % (64 * NW) == 0 || i < XS) {
                 const int L = i & 63, blk = i >> 6; /* blk = tt * 2KP + bb */
+                const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 uint4 h, m, o;
-                xsplit8(xr[k][0], xr[k][1], h, m, o);
+                xsplit8(S.xin[k] ? S.xr[k][0] : z, S.xin[k] ? S.xr[k][1] : z, h, m, o);
                 xl[(blk * 3 + 0) * 64 + L] = h;
                 xl[(blk * 3 + 1) * 64 + L] = m;
                 xl[(blk * 3 + 2) * 64 + L] = o;
@@ -202,10 +209,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
         for (int k = 0; k < DR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
             if (DN % (64 * NW) == 0 || i < DN)
-                dl[i] = dr[k];
+                dl[i] = S.dr[k];
         }
-        __syncthreads();
-
+    };
+    f32x4 acc[RT][MT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+            acc[r][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    /* the MFMAs of the range starting at pair c0, from LDS buffer bf and the stage's weights */
+    auto compute = [&](const stage &S, int bf, long c0) {
+        const uint4 *xl = xls[bf];
+        const uint16_t *dl = dls[bf];
 #pragma unroll
         for (int p = 0; p < KP; p++) {
             const long c = c0 + p;
@@ -216,14 +232,15 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 /* lanes 0-31 hold block 2c, 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
-                const uint32_t a0 = keep ? q[p][r].x : 0u, a1 = keep ? q[p][r].y : 0u, a2 = keep ? q[p][r].z : 0u, a3 = keep ? q[p][r].w : 0u;
+                const uint32_t a0 = keep ? S.q[p][r].x : 0u, a1 = keep ? S.q[p][r].y : 0u, a2 = keep ? S.q[p][r].z : 0u, a3 = keep ? S.q[p][r].w : 0u;
                 const auto s02 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
                 const auto s13 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
                 wb[0][r] = q8_bf16(s02[0], s13[0]);
                 wb[1][r] = q8_bf16(s02[1], s13[1]);
                 const int lr = (wave * RT + r) * 16 + n; /* the lane's row in the workgroup */
-                d[0][r] = ok0 ? q8_half(dl[lr * 2 * KP + 2 * p]) : 0.0f;
-                d[1][r] = ok1 ? q8_half(dl[lr * 2 * KP + 2 * p + 1]) : 0.0f;
+                const float d0 = q8_half(dl[lr * 2 * KP + 2 * p]), d1 = q8_half(dl[lr * 2 * KP + 2 * p + 1]);
+                d[0][r] = ok0 ? d0 : 0.0f;
+                d[1][r] = ok1 ? d1 : 0.0f;
             }
 #pragma unroll
             for (int h = 0; h < 2; h++) {
@@ -236,7 +253,45 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *__restrict__
                 mfma_block<MT, RT>(wb[h], d[h], xa, acc);
             }
         }
-        __syncthreads(); /* every wave done with xl before the next range overwrites it */
+    };
+    /* the pipeline over the split's cps ranges, in chunks of up to GEMM_CHUNK ranges: two
+     * register sets and two LDS buffers taking turns. Issue range ch+1, then commit range ch
+     * (waiting for its x and scales only) and compute it, so two ranges are in flight while the
+     * wave waits. One barrier a range, after the commit: the commit of range ch+1 writes the
+     * other LDS buffer, last read by range ch-1, which every wave finished before it passed the
+     * barrier of range ch. A chunk is unrolled whole (no loop back edge inside it, where the
+     * compiler's wait counting would drain the loads in flight), and a barrier closes it (the
+     * next chunk starts on buffer 0 again). The issue is unconditional (past the chunk's last
+     * range it loads that range again, from L2): under a branch, the wait before the commit
+     * would also wait for the loads just issued. The scheduling barriers keep the compiler from
+     * moving the loads off their place. */
+    const long r0 = (long)split * cps;
+    for (int base = 0; base < cps; base += GEMM_CHUNK) {
+        const int nc = cps - base < GEMM_CHUNK ? cps - base : GEMM_CHUNK;
+        const long rb = r0 + base;
+        stage A, B;
+        __builtin_amdgcn_sched_barrier(0);
+        issue(A, rb * KP);
+#pragma unroll
+        for (int ch = 0; ch < GEMM_CHUNK; ch += 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(B, (rb + (ch + 1 < nc ? ch + 1 : nc - 1)) * KP);
+            __builtin_amdgcn_sched_barrier(0);
+            commit(A, 0);
+            __syncthreads();
+            compute(A, 0, (rb + ch) * KP);
+            if (ch + 1 >= nc)
+                break;
+            __builtin_amdgcn_sched_barrier(0);
+            issue(A, (rb + (ch + 2 < nc ? ch + 2 : nc - 1)) * KP);
+            __builtin_amdgcn_sched_barrier(0);
+            commit(B, 1);
+            __syncthreads();
+            compute(B, 1, (rb + ch + 1) * KP);
+            if (ch + 2 >= nc)
+                break;
+        }
+        __syncthreads(); /* every wave done with both buffers before the next chunk */
     }
     /* lane holds D[token 16(tt0+m) + 4*kq + j][row 16*(rt0+r) + n]: to Y, or to this split's
      * partial, part[split][token][row] over the product's padded tokens (summed by gemm_sum) */
@@ -287,16 +342,21 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
 /* ---------------------------------------------------------------- launchers */
 
 /* The instantiated configurations: MG token tiles a workgroup (the product's MT token tiles in
- * groups of MG, over blockIdx.y), RT row tiles a wave, KP pairs a workgroup, NW waves a workgroup.
- * x in LDS is MG * KP * 6 KiB. */
+ * groups of MG, over blockIdx.y), RT row tiles a wave, KP pairs a range, NW waves a workgroup.
+ * x in LDS is MG * KP * 12 KiB (two ranges). */
 struct gemm_cfg {
     int mg, rt, kp, nw;
 };
-static const gemm_cfg CFGS[] = {{1, 1, 8, 8}, {1, 2, 8, 4}, {1, 1, 8, 4}, {1, 2, 4, 8}, {1, 1, 4, 8}, {1, 1, 16, 8}, {2, 1, 4, 8}, {2, 1, 8, 4}, {2, 2, 4, 4},
-                                {1, 1, 4, 16}, {2, 1, 4, 16}, {1, 1, 2, 16}, {2, 1, 2, 8}};
+#define GEMM_CFGS(X)                                                                                                   \
+    X(1, 1, 4, 8) X(1, 1, 2, 16) X(1, 1, 4, 16) X(1, 1, 8, 8) X(1, 1, 2, 8) X(2, 1, 4, 8) X(2, 1, 2, 8) X(2, 1, 2, 16) \
+        X(2, 1, 4, 16) X(3, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 8) X(4, 1, 2, 16) X(4, 1, 1, 16)
+#define GEMM_CFG_ROW(G, R, P, N) {G, R, P, N},
+static const gemm_cfg CFGS[] = {GEMM_CFGS(GEMM_CFG_ROW)};
+#undef GEMM_CFG_ROW
 #define NCFG ((int)(sizeof(CFGS) / sizeof(CFGS[0])))
 
-/* Q8_GEMM_CFG = "MG,RT,KP,NW" picks an instantiated configuration, for tuning sweeps. */
+/* Q8_GEMM_CFG = "MG,RT,KP,NW" picks an instantiated configuration and Q8_GEMM_KS the K split,
+ * for tuning sweeps. */
 static bool env_cfg(gemm_cfg *c)
 {
     const char *v = getenv("Q8_GEMM_CFG");
@@ -311,26 +371,58 @@ static bool env_cfg(gemm_cfg *c)
     return false;
 }
 
+/* workgroups of an instance resident on the device at once (occupancy x compute units), asked of
+ * the runtime once an instance */
+template <int MG, int RT, int KP, int NW>
+static long gemm_resident()
+{
+    static long n = 0;
+    if (!n) {
+        int per = 0, dev = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, gemm_mfma<MG, RT, KP, NW>, 64 * NW, 0) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per < 1 || cus < 1) {
+            fprintf(stderr, "q8_gemm: occupancy query failed\n");
+            abort();
+        }
+        n = (long)per * cus;
+    }
+    return n;
+}
+
+static long cfg_resident(const gemm_cfg &c)
+{
+#define GEMM_RES(G, R, P, N)                                                                                           \
+    if (c.mg == G && c.rt == R && c.kp == P && c.nw == N)                                                              \
+        return gemm_resident<G, R, P, N>();
+    GEMM_CFGS(GEMM_RES)
+#undef GEMM_RES
+    fprintf(stderr, "q8_gemm: no kernel for MG %d RT %d KP %d NW %d\n", c.mg, c.rt, c.kp, c.nw);
+    abort();
+}
+
 void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *nw, int *ks, int *cps)
 {
-    const long mt = (t + 15) / 16, rt16 = rows / 16;
-    /* measured on the 9B FFN matrices: 4-pair ranges and 8 waves; two token tiles a workgroup
-     * from 17 tokens on */
-    gemm_cfg c = mt == 1 ? CFGS[4] : CFGS[6];
+    const long mt = (t + 15) / 16;
+    /* measured on the 9B FFN matrices (12288 x 4096 and 4096 x 12288): 16 waves and 2-pair
+     * ranges, every token tile in one workgroup, so the weights are read once */
+    gemm_cfg c = mt == 1 ? CFGS[1] : mt == 2 ? CFGS[7] : mt == 3 ? CFGS[10] : CFGS[12];
     gemm_cfg e;
     if (env_cfg(&e) && e.mg <= mt)
         c = e;
-    if (rt16 % c.rt)
-        c = CFGS[0];
     const long tiles = (rows + 16L * c.nw * c.rt - 1) / (16L * c.nw * c.rt);
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
     const long groups = (mt + c.mg - 1) / c.mg;
     const long ranges = (np + c.kp - 1) / c.kp;
-    /* ranges a workgroup: one, unless the partials would not fit the workspace */
-    long per = 1;
+    /* the K split: as many splits as fill the device with one resident round of workgroups, each
+     * streaming cps ranges; fewer if the partials would not fit the workspace */
+    long split = cfg_resident(c) / (tiles * groups);
+    const char *v = getenv("Q8_GEMM_KS");
+    if (v && atol(v) > 0)
+        split = atol(v);
+    split = split < 1 ? 1 : split > ranges ? ranges : split;
+    long per = (ranges + split - 1) / split;
     while (per < ranges && (ranges + per - 1) / per * mt * 16 * rows > Q8_GEMM_PART_MAX)
         per++;
-    (void)tiles, (void)groups;
     *mg = c.mg, *rt = c.rt, *kp = c.kp, *nw = c.nw, *cps = (int)per;
     *ks = (int)((ranges + per - 1) / per);
 }
@@ -364,8 +456,7 @@ void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols
             gemm_sum<<<dim3((unsigned)((t * rows + 255) / 256)), 256, 0, s>>>(part, ks, t, (t + 15) / 16 * 16, rows, y); \
         return;                                                                                                        \
     }
-    GO(1, 1, 8, 8) GO(1, 2, 8, 4) GO(1, 1, 8, 4) GO(1, 2, 4, 8) GO(1, 1, 4, 8) GO(1, 1, 16, 8) GO(2, 1, 4, 8) GO(2, 1, 8, 4) GO(2, 2, 4, 4)
-    GO(1, 1, 4, 16) GO(2, 1, 4, 16) GO(1, 1, 2, 16) GO(2, 1, 2, 8)
+    GEMM_CFGS(GO)
 #undef GO
     fprintf(stderr, "q8_gemm: no kernel for MG %d RT %d KP %d NW %d\n", mg, rt, kp, nw);
     abort();
