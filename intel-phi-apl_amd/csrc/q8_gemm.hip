@@ -265,9 +265,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
      * range it loads that range again, from L2): under a branch, the wait before the commit
      * would also wait for the loads just issued. The scheduling barriers keep the compiler from
      * moving the loads off their place. */
-    const long r0 = (long)split * cps;
-    for (int base = 0; base < cps; base += GEMM_CHUNK) {
-        const int nc = cps - base < GEMM_CHUNK ? cps - base : GEMM_CHUNK;
+    const long r0 = (long)split * cps, nr = (np + KP - 1) / KP;
+    const int mine = (int)(nr - r0 < cps ? nr - r0 : cps); /* the last split may hold fewer ranges */
+    for (int base = 0; base < mine; base += GEMM_CHUNK) {
+        const int nc = mine - base < GEMM_CHUNK ? mine - base : GEMM_CHUNK;
         const long rb = r0 + base;
         stage A, B;
         __builtin_amdgcn_sched_barrier(0);
