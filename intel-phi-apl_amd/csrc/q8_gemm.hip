@@ -16,10 +16,11 @@
  * lane needs the scale of one row per block. Within a block the lane groups hold the columns
  * KCOL(kq) .. +7 (below), in both operands.
  *
- *   gemm_mfma   a workgroup of NW waves owns NW row tiles of 16 rows and KP pairs of blocks; it
- *               loads the range's x (split into limbs on the way into LDS), its rows' scales (into
- *               LDS) and every weight of every wave at once, then runs the MFMAs. With the K range
- *               split over ks workgroups, each writes a partial;
+ *   gemm_mfma   a workgroup of NW waves owns NW row tiles of 16 rows, its token tiles and a K
+ *               slice of cps ranges of KP block pairs, which it streams: for each range it loads x
+ *               (split into limbs on the way into LDS), its rows' scales (into LDS) and every weight
+ *               of every wave, with the next range's loads in flight during this one's wait and
+ *               MFMAs. With K split over ks workgroups, each writes a partial;
  *   gemm_sum    adds the ks partials in split order: the same order every run, deterministic. */
 #include <hip/hip_runtime.h>
 
