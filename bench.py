@@ -336,6 +336,41 @@ def host_pointers(b):
     return out
 
 
+def gguf_load(b):
+    """The GGUF load path: a file holding one 9B layer's five Q8_0 matrices (QKV 6144x4096, out
+    4096x4096, gate and up 12288x4096, down 4096x12288: 205 MB) read by rt_gguf_read and uploaded by
+    rt_gguf_upload (pread into pinned chunks, copy, repack to form S on the GPU), from the page
+    cache. The reference repacks the same bytes in place on its CPU team instead (engine.c:303-316)."""
+    import shutil
+    import tempfile
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_file as gf
+
+    F, H, Q = 12288, HIDDEN, 6144
+    shapes = [("blk.0.attn_qkv.weight", Q, H), ("blk.0.attn_output.weight", H, H), ("blk.0.ffn_gate.weight", F, H),
+              ("blk.0.ffn_up.weight", F, H), ("blk.0.ffn_down.weight", H, F)]
+    rng = np.random.default_rng(5)
+    tensors = [{"name": n, "dims": [k, r], "type": gf.Q8_0, "data": rng.integers(0, 256, r * k // 32 * 34, dtype=np.uint8).tobytes()}
+               for n, r, k in shapes]
+    d = tempfile.mkdtemp(prefix="q8gguf")
+    try:
+        path = os.path.join(d, "layer.gguf")
+        gf.write(path, [("general.architecture", gf.STR, "qwen35")], tensors)
+        times = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            g = b.q8rt.GGUF(path)
+            g.upload(b.rt)
+            times.append(time.perf_counter() - t0)
+            nbytes = g.h.q8_bytes
+            g.close()
+        s = statistics.median(times)
+        return {"bytes": nbytes, "ms": round(s * 1e3, 2), "GB/s": round(nbytes / s / 1e9, 2), "runs": len(times)}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def layers_2b(b):
     """Config 2: 24 layers of QKV 3072x2048, out 2048x2048, gate/up 6144x2048 (fused), down 2048x6144."""
     H, F, Q = 2048, 6144, 2048 + 2 * 512
@@ -600,7 +635,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", metavar="SECTIONS", help="comma-separated sections to run instead of the full line (gemv_4096x4096, "
-                    "draft_head, prompt_gemm, verify, 2b_layer_set); prints their results only")
+                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, gguf_load_9b_layer); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
     ap.add_argument("--summarize-gemm", metavar="DIR", help="write the GEMM rocprofv3 summary under profiles/ from DIR and exit")
@@ -622,7 +657,8 @@ def main():
     name, cus = b.rt.device_info()
     log(f"device: {name}, {cus} CUs")
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
-                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers))
+                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers),
+                ("gguf_load_9b_layer", gguf_load))
     if a.only:
         want = a.only.split(",")
         for key, fn in sections:

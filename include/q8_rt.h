@@ -102,6 +102,11 @@ void gemv_i_repack(const uint8_t *q8, long rows, long cols, void *out);
  * `w`. Call once per distinct tensor (tied tensors share a handle, engine.c:307-310). The
  * host buffer may be freed on return. NULL when HBM is full. */
 const void *rt_q8_upload(struct rt *R, const uint8_t *q8, long rows, long cols);
+/* Addition (no reference counterpart; the GGUF loader's path): the same for GGUF Q8_0 rows read
+ * from an open file at byte `offset`, straight into pinned staging in chunks of whole 16-row
+ * groups (64 MiB, or Q8_UPLOAD_CHUNK bytes), each repacked on the device while the next is read.
+ * NULL when HBM is full or a read fails (errno set). */
+const void *rt_q8_upload_fd(struct rt *R, int fd, uint64_t offset, long rows, long cols);
 /* The same for a matrix already in form S in host memory (gemv_i_repack's output). */
 const void *rt_q8_upload_packed(struct rt *R, const void *packed, long rows, long cols);
 /* Frees an uploaded matrix. */

@@ -7,15 +7,17 @@ is an error (RuntimeError), never a fallback.
 
 Reference interface mirrored: src/card/rt.h:19-26 (struct rt), 38-39 (rt_init), 61-72
 (rt_gemv, rt_gemv_q, rt_gemv_open, rt_gemv_go, rt_gemm, rt_gemm_q); src/card/gemv.h:50-57
-(gemv_i_bytes, gemv_i_repack).
+(gemv_i_bytes, gemv_i_repack); src/host/gguf_reader.h:17-58 (the GGUF header reader, as
+rt_gguf_*, include/q8_gguf.h) and src/card/engine.c:287-316 (the load loop, rt_gguf_upload).
 """
+import glob
 import ctypes
 import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libq8rt.so")
-HEADER = os.path.join(os.path.dirname(HERE), "include", "q8_rt.h")
+HEADERS = sorted(glob.glob(os.path.join(os.path.dirname(HERE), "include", "*.h")))
 
 _c = ctypes
 _vp, _long, _int, _f32p, _u64 = _c.c_void_p, _c.c_long, _c.c_int, _c.c_void_p, _c.c_uint64
@@ -69,15 +71,50 @@ _SIGS = {
     "rt_graph_free": (None, [_vp, _vp]),
     "rt_ktime": (None, [_vp, _int]),
     "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _long]),
+    "rt_q8_upload_fd": (_vp, [_vp, _int, _u64, _long, _long]),
+    "rt_gguf_read": (_int, [_vp, _c.c_char_p, _c.c_char_p, _c.c_size_t]),
+    "rt_gguf_free": (None, [_vp]),
+    "rt_gguf_key": (_vp, [_vp, _c.c_char_p]),
+    "rt_gguf_tensor": (_vp, [_vp, _c.c_char_p]),
+    "rt_gguf_tensor_at": (_vp, [_vp, _u64]),
+    "rt_gguf_key_u64": (_u64, [_vp, _c.c_char_p, _u64]),
+    "rt_gguf_value_type_name": (_c.c_char_p, [_c.c_uint32]),
+    "rt_gguf_tensor_type_name": (_c.c_char_p, [_c.c_uint32]),
+    "rt_gguf_upload": (_int, [_vp, _vp, _c.c_char_p, _c.c_char_p, _c.c_size_t]),
+    "rt_gguf_release": (None, [_vp, _vp]),
 }
+
+
+class GgufKey(_c.Structure):
+    """struct rt_gguf_key (include/q8_gguf.h; gguf_reader.h:17-23)."""
+
+    _fields_ = [("name", _c.c_char * 96), ("type", _c.c_uint32), ("elem_type", _c.c_uint32), ("n", _u64), ("text", _c.c_char * 128)]
+
+
+class GgufTensor(_c.Structure):
+    """struct rt_gguf_tensor (include/q8_gguf.h; gguf_reader.h:25-32, plus the HBM handle)."""
+
+    _fields_ = [("name", _c.c_char * 96), ("n_dims", _c.c_uint32), ("dim", _u64 * 4), ("type", _c.c_uint32), ("offset", _u64), ("bytes", _u64),
+                ("w", _vp)]
+
+
+class GgufHeader(_c.Structure):
+    """struct rt_gguf (include/q8_gguf.h; gguf_reader.h:34-43, plus the upload's totals)."""
+
+    _fields_ = [("version", _c.c_uint32), ("file_size", _u64), ("header_end", _u64), ("data_start", _u64), ("data_bytes", _u64), ("need", _u64),
+                ("n_keys", _u64), ("n_tensors", _u64), ("keys", _c.POINTER(GgufKey)), ("tensors", _c.POINTER(GgufTensor)), ("q8_bytes", _u64),
+                ("q8_count", _int)]
 
 KINDS = {0: "gemv", 1: "gemv_pair", 2: "gemm", 3: "gemm_pair", 4: "exact", 5: "round"}
 
 
-def header_symbols(path=HEADER):
-    """Every function name include/q8_rt.h declares."""
-    text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
-    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(\w+)\s*\(", text, flags=re.M)) - {"defined"})
+def header_symbols(paths=None):
+    """Every function name the headers under include/ declare."""
+    names = set()
+    for path in paths or HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+        names |= set(re.findall(r"^[A-Za-z_][\w \*]*?\b(\w+)\s*\(", text, flags=re.M))
+    return sorted(names - {"defined"})
 
 
 _lib = None
@@ -180,3 +217,70 @@ class Runtime:
         cus = _int(0)
         self.lib.rt_device_info(self.R, name, 256, _c.byref(cus))
         return name.value.decode(), cus.value
+
+
+class GGUF:
+    """A GGUF file's header and tensor table (rt_gguf_read) and, after upload(runtime), the HBM
+    handles of its Q8_0 tensors (rt_gguf_upload: one per distinct file offset, so tensors tied by
+    offset share one). A bad file raises ValueError with the library's "path: reason"."""
+
+    def __init__(self, path):
+        self.lib = load()
+        self.path = os.fsencode(path)
+        self.h = GgufHeader()
+        self.runtime = None
+        err = _c.create_string_buffer(512)
+        if self.lib.rt_gguf_read(_c.byref(self.h), self.path, err, 512) != 0:
+            raise ValueError(err.value.decode())
+
+    @staticmethod
+    def _key(k):
+        return {"name": k.name.decode(), "type": k.type, "elem_type": k.elem_type, "n": k.n, "text": k.text.decode()}
+
+    @staticmethod
+    def _tensor(t):
+        return {"name": t.name.decode(), "n_dims": t.n_dims, "dim": list(t.dim), "type": t.type, "offset": t.offset, "bytes": t.bytes,
+                "w": t.w}
+
+    def keys(self):
+        return [self._key(self.h.keys[i]) for i in range(self.h.n_keys)]
+
+    def tensors(self):
+        return [self._tensor(self.h.tensors[i]) for i in range(self.h.n_tensors)]
+
+    def tensor(self, name):
+        p = self.lib.rt_gguf_tensor(_c.byref(self.h), name.encode())
+        return self._tensor(GgufTensor.from_address(p)) if p else None
+
+    def tensor_at(self, offset):
+        p = self.lib.rt_gguf_tensor_at(_c.byref(self.h), offset)
+        return self._tensor(GgufTensor.from_address(p)) if p else None
+
+    def key(self, name):
+        p = self.lib.rt_gguf_key(_c.byref(self.h), name.encode())
+        return self._key(GgufKey.from_address(p)) if p else None
+
+    def key_u64(self, name, fallback=0):
+        return self.lib.rt_gguf_key_u64(_c.byref(self.h), name.encode(), fallback)
+
+    def upload(self, runtime):
+        """Every Q8_0 tensor to HBM; RuntimeError with the reason (nothing left uploaded) if not."""
+        err = _c.create_string_buffer(512)
+        if self.lib.rt_gguf_upload(runtime.R, _c.byref(self.h), self.path, err, 512) != 0:
+            raise RuntimeError(err.value.decode())
+        self.runtime = runtime
+
+    def release(self):
+        if self.runtime is not None:
+            self.lib.rt_gguf_release(self.runtime.R, _c.byref(self.h))
+            self.runtime = None
+
+    def close(self):
+        self.release()
+        self.lib.rt_gguf_free(_c.byref(self.h))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -7,9 +7,11 @@
  * one copy of every y back, one wait. */
 #include <hip/hip_runtime.h>
 
+#include <errno.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <unordered_map>
 #include <vector>
@@ -74,6 +76,11 @@ struct ctx {
     std::unordered_map<const void *, matrix> weights;
     job queue[RT_BATCH];
     int queued = 0;
+    /* weight upload staging: two pinned host chunks and two device chunks of whole 16-row groups,
+     * an event per chunk slot (the slot's copy and repack are done); allocated on the first upload */
+    uint8_t *up_host[2] = {nullptr, nullptr}, *up_dev[2] = {nullptr, nullptr};
+    hipEvent_t up_done[2] = {nullptr, nullptr};
+    size_t up_cap = 0;
     /* kernel timing (rt_ktime): one event pair per recorded product */
     int ktime_on = 0;
     std::vector<hipEvent_t> kt_events;
@@ -381,6 +388,14 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipEventDestroy(e));
     if (c->amax)
         HIPCHECK(hipFree(c->amax));
+    for (int k = 0; k < 2; k++) {
+        if (c->up_host[k])
+            HIPCHECK(hipHostFree(c->up_host[k]));
+        if (c->up_dev[k])
+            HIPCHECK(hipFree(c->up_dev[k]));
+        if (c->up_done[k])
+            HIPCHECK(hipEventDestroy(c->up_done[k]));
+    }
     if (current == c)
         current = nullptr;
     HIPCHECK(hipEventDestroy(c->ev0));
@@ -467,25 +482,106 @@ static const void *register_matrix(ctx *c, void *dev, long rows, long cols)
     return dev;
 }
 
+extern "C++" {
+/* Bytes of an upload chunk: Q8_UPLOAD_CHUNK (bytes) or 64 MiB; at least one 16-row group. */
+static size_t upload_chunk(size_t group)
+{
+    const char *v = getenv("Q8_UPLOAD_CHUNK");
+    size_t n = v && atol(v) > 0 ? (size_t)atol(v) : (size_t)64 << 20;
+    return n < group ? group : n;
+}
+
+static void reserve_upload(ctx *c, size_t group)
+{
+    const size_t need = upload_chunk(group);
+    if (c->up_cap >= need)
+        return;
+    no_capture(c, "the upload staging");
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    for (int k = 0; k < 2; k++) {
+        if (c->up_host[k])
+            HIPCHECK(hipHostFree(c->up_host[k]));
+        if (c->up_dev[k])
+            HIPCHECK(hipFree(c->up_dev[k]));
+        HIPCHECK(hipHostMalloc((void **)&c->up_host[k], need, hipHostMallocDefault));
+        HIPCHECK(hipMalloc((void **)&c->up_dev[k], need));
+        if (!c->up_done[k])
+            HIPCHECK(hipEventCreateWithFlags(&c->up_done[k], hipEventDisableTiming));
+    }
+    c->up_cap = need;
+}
+
+/* A new form S matrix of rows x cols from GGUF Q8_0 rows, chunk by chunk: read(dst, off, n) puts
+ * the source's bytes [off, off + n) into a pinned chunk, which goes to HBM and is repacked there
+ * (a run of whole 16-row groups is a form S matrix of its own, at the same byte offset) while the
+ * host fills the other chunk. nullptr, with nothing left allocated, when HBM is full or a read
+ * fails (*read_failed set). */
+template <class Read>
+static const void *upload_groups(ctx *c, const char *fn, long rows, long cols, Read read, bool *read_failed)
+{
+    no_capture(c, fn);
+    const size_t bytes = (size_t)gemv_i_bytes(rows, cols), group = (size_t)gemv_i_bytes(Q8_GROUP, cols);
+    reserve_upload(c, group);
+    const size_t want = upload_chunk(group), per = (want < c->up_cap ? want : c->up_cap) / group * group;
+    void *out = nullptr;
+    if (hipMalloc(&out, bytes) != hipSuccess)
+        return nullptr;
+    int k = 0;
+    for (size_t off = 0; off < bytes; off += per, k ^= 1) {
+        const size_t n = bytes - off < per ? bytes - off : per;
+        HIPCHECK(hipEventSynchronize(c->up_done[k])); /* the slot's last copy has read its chunk */
+        if (!read(c->up_host[k], off, n)) {
+            HIPCHECK(hipStreamSynchronize(c->stream));
+            HIPCHECK(hipFree(out));
+            *read_failed = true;
+            return nullptr;
+        }
+        HIPCHECK(hipMemcpyAsync(c->up_dev[k], c->up_host[k], n, hipMemcpyHostToDevice, c->stream));
+        q8_launch_repack((q8_stream_t)c->stream, c->up_dev[k], (long)(n / group) * Q8_GROUP, cols, (uint8_t *)out + off);
+        launched("the repack");
+        HIPCHECK(hipEventRecord(c->up_done[k], c->stream));
+    }
+    HIPCHECK(hipStreamSynchronize(c->stream));
+    return register_matrix(c, out, rows, cols);
+}
+} /* extern "C++" */
+
 const void *rt_q8_upload(struct rt *R, const uint8_t *q8, long rows, long cols)
 {
     ctx *c = get(R, "rt_q8_upload");
     if (!q8 || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK)
         fail("rt_q8_upload", "needs q8, rows a positive multiple of 16, cols of 32");
-    const size_t bytes = (size_t)gemv_i_bytes(rows, cols);
-    void *raw = nullptr, *out = nullptr;
-    if (hipMalloc(&out, bytes) != hipSuccess)
-        return nullptr;
-    if (hipMalloc(&raw, bytes) != hipSuccess) {
-        HIPCHECK(hipFree(out));
-        return nullptr;
-    }
-    HIPCHECK(hipMemcpyAsync(raw, q8, bytes, hipMemcpyHostToDevice, c->stream));
-    q8_launch_repack((q8_stream_t)c->stream, raw, rows, cols, out);
-    launched("the repack");
-    HIPCHECK(hipStreamSynchronize(c->stream));
-    HIPCHECK(hipFree(raw));
-    return register_matrix(c, out, rows, cols);
+    bool bad = false;
+    return upload_groups(
+        c, "rt_q8_upload", rows, cols,
+        [&](uint8_t *dst, size_t off, size_t n) {
+            memcpy(dst, q8 + off, n);
+            return true;
+        },
+        &bad);
+}
+
+const void *rt_q8_upload_fd(struct rt *R, int fd, uint64_t offset, long rows, long cols)
+{
+    ctx *c = get(R, "rt_q8_upload_fd");
+    if (fd < 0 || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK)
+        fail("rt_q8_upload_fd", "needs an open file, rows a positive multiple of 16, cols of 32");
+    bool bad = false;
+    const void *w = upload_groups(
+        c, "rt_q8_upload_fd", rows, cols,
+        [&](uint8_t *dst, size_t off, size_t n) {
+            for (size_t got = 0; got < n;) {
+                const ssize_t r = pread(fd, dst + got, n - got, (off_t)(offset + off + got));
+                if (r <= 0)
+                    return false;
+                got += (size_t)r;
+            }
+            return true;
+        },
+        &bad);
+    if (!w)
+        errno = bad ? (errno ? errno : EIO) : ENOMEM;
+    return w;
 }
 
 const void *rt_q8_upload_packed(struct rt *R, const void *packed, long rows, long cols)
