@@ -336,6 +336,58 @@ def host_pointers(b):
     return out
 
 
+def epilogues_9b(b):
+    """The 9B decode layer with the epilogues around its products (src/apl/qwen35.apl:131-139): QKV
+    and the gate+up pair on RMS(x), the output and down products added to the residual stream,
+    32 layers recorded as one graph, three ways: the products alone (4 launches a layer), with the
+    epilogues fused into them (4), and with the norms and adds as kernels of their own (8,
+    Q8_EPI_APART=1). Weights rotate through 32 layers (7.2 GB), as in the token."""
+    eps = 1e-6
+    layers = [(b.matrix(QKV, HIDDEN), b.matrix(HIDDEN, HIDDEN), b.matrix(FFN, HIDDEN), b.matrix(FFN, HIDDEN), b.matrix(HIDDEN, FFN))
+              for _ in range(LAYERS)]
+    x, xa, nw1, nw2, q, h, y = b.vec(HIDDEN), b.vec(HIDDEN), b.vec(HIDDEN), b.vec(HIDDEN), b.vec(QKV), b.vec(FFN), b.vec(HIDDEN)
+    L, R, V = b.lib, b.R, c.c_void_p
+
+    def bare():
+        for qkv, o, g, u, d in layers:
+            b.gemm(qkv, QKV, HIDDEN, x, 1, q)
+            b.gemm(o, HIDDEN, HIDDEN, xa, 1, y)
+            b.pair(g, u, FFN, HIDDEN, x, 1, h)
+            b.gemm(d, HIDDEN, FFN, h, 1, y)
+
+    def with_epilogues():
+        for qkv, o, g, u, d in layers:
+            L.rt_gemm_norm_dev(R, V(qkv), QKV, HIDDEN, V(x), HIDDEN, 1, V(nw1), eps, V(q))
+            L.rt_gemm_residual_dev(R, V(o), HIDDEN, HIDDEN, V(xa), HIDDEN, 1, V(x), V(x))
+            L.rt_gemv_swiglu_norm_dev(R, V(g), V(u), FFN, HIDDEN, V(x), HIDDEN, 1, V(nw2), eps, V(h))
+            L.rt_gemm_residual_dev(R, V(d), HIDDEN, FFN, V(h), FFN, 1, V(x), V(x))
+
+    per = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) + alg_bytes(HIDDEN, FFN, 1))
+    out = {"bytes_32_layers": per}
+    for key, fn, apart in (("products_only", bare, False), ("epilogues_fused", with_epilogues, False), ("epilogues_apart", with_epilogues, True)):
+        if apart:
+            os.environ["Q8_EPI_APART"] = "1"
+        try:
+            fn()
+            b.rt.sync()
+            L.rt_graph_begin(R)
+            fn()
+            g = L.rt_graph_end(R)
+            L.rt_graph_launch(R, c.c_void_p(g))
+            ms = b.timed(lambda: L.rt_graph_launch(R, c.c_void_p(g)), 20)
+            L.rt_graph_free(R, c.c_void_p(g))
+        finally:
+            os.environ.pop("Q8_EPI_APART", None)
+        out[key] = {"us_per_32_layers": round(1e3 * ms, 2), "GB/s": round(per / ms / 1e6, 1)}
+    out["fused_saves_us_per_layer"] = round((out["epilogues_apart"]["us_per_32_layers"] - out["epilogues_fused"]["us_per_32_layers"]) / LAYERS, 3)
+    for Lw in layers:
+        for w in Lw:
+            b.rt.free(w)
+    for p in (x, xa, nw1, nw2, q, h, y):
+        b.rt.free(p)
+    return out
+
+
 def gguf_load(b):
     """The GGUF load path: a file holding one 9B layer's five Q8_0 matrices (QKV 6144x4096, out
     4096x4096, gate and up 12288x4096, down 4096x12288: 205 MB) read by rt_gguf_read and uploaded by
@@ -635,7 +687,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", metavar="SECTIONS", help="comma-separated sections to run instead of the full line (gemv_4096x4096, "
-                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, gguf_load_9b_layer); prints their results only")
+                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, gguf_load_9b_layer, epilogues_9b); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
     ap.add_argument("--summarize-gemm", metavar="DIR", help="write the GEMM rocprofv3 summary under profiles/ from DIR and exit")
@@ -658,7 +710,7 @@ def main():
     log(f"device: {name}, {cus} CUs")
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
                 ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers),
-                ("gguf_load_9b_layer", gguf_load))
+                ("gguf_load_9b_layer", gguf_load), ("epilogues_9b", epilogues_9b))
     if a.only:
         want = a.only.split(",")
         for key, fn in sections:

@@ -134,6 +134,28 @@ void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *ro
 /* The FFN's fused pair: Y[k] = SiLU(G[k]) * U[k] with G = X Wg^T and U = X Wu^T, both [rows cols],
  * x read once for both; SiLU(g) = g / (1 + exp(-g)) (src/apl/qwen35.apl:38, 125). t tokens. */
 void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* ---- the epilogues on either side of a product (additions; the reference computes them on its
+ * host around the products: RMS = {⍺×⍵×(RMS_EPS+(+/⍵×⍵)÷≢⍵)*¯0.5}, src/apl/qwen35.apl:49, before a
+ * layer's mixer and FFN, and the residual Z←X+… after them, qwen35.apl:131-139). Fused into the
+ * decode kernel (t <= 4) for K = 2048, 4096, 6144 and 12288, the residual into the matrix-core
+ * product's store for t >= 5; other shapes run the norm or the add as a kernel of its own. The
+ * norm is s = 1 / sqrt(eps + sum_k x[k]^2 / cols) per token in F32, xn[k] = nw[k] * (x[k] * s); its
+ * sum runs in a fixed order for a given shape, so results repeat bit for bit, and a fused and a
+ * separate norm differ only by that order (an ulp or so of s). The residual is one F32 add of the
+ * product, the same bits fused or apart. */
+/* xn = the normed x, t tokens (x rows x_stride floats apart, xn rows cols apart; xn may be x when
+ * x_stride == cols); cols % 4 == 0. */
+void rt_rmsnorm_dev(struct rt *R, const float *x, long x_stride, long t, long cols, const float *nw, float eps, float *xn);
+/* Y = RMS(X) W^T: the normed x is never stored. */
+void rt_gemm_norm_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, const float *nw, float eps, float *y);
+/* The fused pair on RMS(X): Y = SiLU(RMS(X) Wg^T) * (RMS(X) Wu^T) (W_PNORM RMS then the FFN, qwen35.apl:125, 132). */
+void rt_gemv_swiglu_norm_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, const float *nw,
+                             float eps, float *y);
+/* A round of products sharing RMS(X) (the DeltaNet quartet on W_ANORM RMS X), one launch. */
+void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
+                            const float *nw, float eps, float *const *y);
+/* Y = R + X W^T (after W_OUT and W_DOWN); r [t rows] may be y, the residual stream updated in place. */
+void rt_gemm_residual_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, const float *r, float *y);
 /* z[i*cols ..] = row rows[i] of w dequantised, i < n (rows: device longs, each < the matrix's
  * rows; z device). The embedding read of a batch of tokens. An addition. */
 void rt_q8_rows_dev(struct rt *R, const void *w, long cols, const long *rows, long n, float *z);

@@ -72,6 +72,11 @@ _SIGS = {
     "rt_ktime": (None, [_vp, _int]),
     "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _long]),
     "rt_q8_upload_fd": (_vp, [_vp, _int, _u64, _long, _long]),
+    "rt_rmsnorm_dev": (None, [_vp, _vp, _long, _long, _long, _vp, _c.c_float, _vp]),
+    "rt_gemm_norm_dev": (None, [_vp, _vp, _long, _long, _vp, _long, _long, _vp, _c.c_float, _vp]),
+    "rt_gemv_swiglu_norm_dev": (None, [_vp, _vp, _vp, _long, _long, _vp, _long, _long, _vp, _c.c_float, _vp]),
+    "rt_gemv_round_norm_dev": (None, [_vp, _int, _vp, _vp, _long, _vp, _long, _long, _vp, _c.c_float, _vp]),
+    "rt_gemm_residual_dev": (None, [_vp, _vp, _long, _long, _vp, _long, _long, _vp, _vp]),
     "rt_gguf_read": (_int, [_vp, _c.c_char_p, _c.c_char_p, _c.c_size_t]),
     "rt_gguf_free": (None, [_vp]),
     "rt_gguf_key": (_vp, [_vp, _c.c_char_p]),

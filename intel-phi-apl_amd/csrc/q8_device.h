@@ -116,6 +116,23 @@ extern long *q8_next_grid;
 
 /* Y = X W^T, t tokens, the fast kernels; W form S. w1 != NULL: the fused pair, Y = SiLU(X W0^T) * (X W1^T). */
 void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* An epilogue on either side of a product (src/apl/qwen35.apl:49, 131-139). nw != NULL: the RMS
+ * norm first, per token xn[k] = nw[k] * (x[k] * s) with s = 1 / sqrt(eps + sum_k x[k]^2 / cols);
+ * res != NULL: Y = res + the product, res laid out as Y (it may be Y: the residual stream updated
+ * in place). One of the two at a time. */
+struct q8_epi {
+    const float *nw;
+    float eps;
+    const float *res;
+};
+/* The decode product with the epilogue fused into its kernel (t <= 4): 0, or -1 when no fused
+ * kernel takes the shape (nothing launched; the caller runs the epilogue apart). */
+int q8_launch_gemv_epi(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y,
+                       q8_epi e);
+/* The RMS norm apart: xn [t cols] (rows cols floats apart) from x [t cols] (x_stride apart). */
+void q8_launch_rmsnorm(q8_stream_t stream, const float *x, long x_stride, long t, long cols, const float *nw, float eps, float *xn);
+/* y[i] = a[i] + b[i], i < n (y may be a or b). */
+void q8_launch_add(q8_stream_t stream, const float *a, const float *b, long n, float *y);
 /* A round of products sharing x as one launch (t <= 4, cols % 1024 == 0, every rows % 8 == 0):
  * 0, or -1 (nothing launched: the caller runs them one by one). */
 #define Q8_ROUND_MAX 8
@@ -127,12 +144,16 @@ struct q8_round {
     long start[Q8_ROUND_MAX + 1]; /* first workgroup of each product; start[n] = the grid */
 };
 int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
+/* The same with the RMS norm of x fused (e.nw != NULL, e.res NULL): 0, or -1 (nothing launched). */
+int q8_launch_gemv_round_epi(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
+                             float *const *y, q8_epi e);
 /* The reference's order, every y bit-identical to the reference's F32 host path. */
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* Y = X W^T for 5 <= t <= 64 on the matrix cores (and the sum of the K split's partials). part
  * holds q8_gemm_part_floats(rows, cols, t) floats, at most Q8_GEMM_PART_MAX. */
 #define Q8_GEMM_PART_MAX (8L << 20)
-void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part);
+void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
+                         const float *res = nullptr);
 long q8_gemm_part_floats(long rows, long cols, long t);
 /* the kernel's choice for a shape: MG token tiles, RT row tiles a wave, KP pairs of blocks and NW
  * waves a workgroup, ks workgroups along K, cps ranges of KP pairs a workgroup */

@@ -135,7 +135,7 @@ struct gemm_stage {
  * The ks workgroups of a row tile write partials that gemm_sum adds in split order. */
 template <int MT, int RT, int KP, int NW>
 __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
-                                                     float *part, float *y)
+                                                     float *part, float *y, const float *res)
 {
     typedef gemm_stage<MT, RT, KP, NW> stage;
     constexpr int XS = stage::XS, XR = stage::XR, DN = stage::DN, DR = stage::DR;
@@ -295,8 +295,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
         }
         __syncthreads(); /* every wave done with both buffers before the next chunk */
     }
-    /* lane holds D[token 16(tt0+m) + 4*kq + j][row 16*(rt0+r) + n]: to Y, or to this split's
-     * partial, part[split][token][row] over the product's padded tokens (summed by gemm_sum) */
+    /* lane holds D[token 16(tt0+m) + 4*kq + j][row 16*(rt0+r) + n]: to Y (plus the residual when
+     * res is given), or to this split's partial, part[split][token][row] over the product's padded
+     * tokens (summed by gemm_sum) */
     if (!live)
         return;
     const long tp = (t + 15) / 16 * 16;
@@ -308,8 +309,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
             for (int j = 0; j < 4; j++) {
                 const long tok = 16 * (tt0 + m) + 4 * kq + j;
                 if (ks == 1) {
+                    const long i = tok * rows + (rt0 + r) * 16 + n;
                     if (tok < t)
-                        y[tok * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
+                        y[i] = res ? res[i] + acc[r][m][j] : acc[r][m][j];
                 } else if (tok < tp) {
                     part[((long)split * tp + tok) * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
                 }
@@ -317,8 +319,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
 }
 
 /* Y = the sum of the ks partials in split order, one thread an output (the kernel boundary
- * before it makes every split's stores visible) */
-__global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *__restrict__ y)
+ * before it makes every split's stores visible), plus the residual when res is given (res may be Y) */
+__global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *y, const float *res)
 {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= t * rows)
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
     }
     for (; s < ks; s++)
         v += part[(long)s * step + i];
-    y[i] = v;
+    y[i] = res ? res[i] + v : v;
 }
 
 /* ---------------------------------------------------------------- launchers */
@@ -437,15 +439,17 @@ long q8_gemm_part_floats(long rows, long cols, long t)
 }
 
 template <int MG, int RT, int KP, int NW>
-static void gemm_go(hipStream_t s, const void *w, long rows, long cols, const float *x, long xst, long t, float *y, float *part, int ks, int cps)
+static void gemm_go(hipStream_t s, const void *w, long rows, long cols, const float *x, long xst, long t, float *y, float *part, int ks, int cps,
+                    const float *res)
 {
     const long tiles = (rows + 16L * NW * RT - 1) / (16L * NW * RT);
     const long groups = ((t + 15) / 16 + MG - 1) / MG;
     Q8_LAUNCH(q8_time_name("gemm_mfma", 4, MG, RT, KP, NW), (gemm_mfma<MG, RT, KP, NW>), dim3((unsigned)(tiles * ks), (unsigned)groups),
-              dim3(64 * NW), s, (const uint8_t *)w, rows, cols, x, xst, t, ks, cps, part, y);
+              dim3(64 * NW), s, (const uint8_t *)w, rows, cols, x, xst, t, ks, cps, part, y, res);
 }
 
-void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part)
+void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
+                         const float *res)
 {
     hipStream_t s = (hipStream_t)stream;
     int mg, rt, kp, nw, ks, cps;
@@ -453,9 +457,9 @@ void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols
     float *out = ks > 1 ? part : y;
 #define GO(G, R, P, N)                                                                                                 \
     if (mg == G && rt == R && kp == P && nw == N) {                                                                    \
-        gemm_go<G, R, P, N>(s, w, rows, cols, x, x_stride, t, out, part, ks, cps);                                      \
+        gemm_go<G, R, P, N>(s, w, rows, cols, x, x_stride, t, out, part, ks, cps, ks > 1 ? nullptr : res);              \
         if (ks > 1)                                                                                                    \
-            gemm_sum<<<dim3((unsigned)((t * rows + 255) / 256)), 256, 0, s>>>(part, ks, t, (t + 15) / 16 * 16, rows, y); \
+            gemm_sum<<<dim3((unsigned)((t * rows + 255) / 256)), 256, 0, s>>>(part, ks, t, (t + 15) / 16 * 16, rows, y, res); \
         return;                                                                                                        \
     }
     GEMM_CFGS(GO)

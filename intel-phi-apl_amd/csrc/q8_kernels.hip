@@ -143,9 +143,11 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_s(const uint8_t *__restr
  * otherwise. Per unit: 16 exact int8->f32 converts shared by the MT tokens, a 16-step fma chain
  * per token, then acc = fma(s, d, acc) with the unit's block scale. The lanes' partials are summed
  * by q8_wave_sum_dpp, the NW waves' in LDS in wave order: the same order every run. */
-template <int MT, int RW, int S, int NW, int PAIR>
+/* EPI: 0 none; 1 the RMS norm of x first (e.nw, e.eps); 2 y = e.res + the product (q8_epi). y and
+ * e.res may be the same array: each element is read and then written by the one thread that owns it. */
+template <int MT, int RW, int S, int NW, int PAIR, int EPI>
 __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols, const float *__restrict__ x,
-                                          long x_stride, float *__restrict__ y, long r0)
+                                          long x_stride, float *y, long r0, q8_epi e)
 {
     constexpr int P = PAIR + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -159,6 +161,24 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
 #pragma unroll
             for (int c = 0; c < 4; c++)
                 xv[m][s][c] = *(const float4 *)(x + m * x_stride + 16 * (u0 + 64 * s) + 4 * c);
+    /* the residual of the output this thread stores (thread k < RW*MT stores row k / MT, token
+     * k % MT; the others load one of those too, so the load is unconditional), issued with x so
+     * that it is not a memory latency at the kernel's end */
+    float rv = 0.0f;
+    if constexpr (EPI == 2) {
+        static_assert(NW > 1, "the residual epilogue stores from threads < RW * MT");
+        const int k = (int)threadIdx.x % (RW * MT);
+        rv = e.res[(long)(k % MT) * rows + r0 + k / MT];
+    }
+    /* the norm's weights, the lane's columns, issued with x before the matrix */
+    float4 nv[S][4];
+    if constexpr (EPI == 1) {
+#pragma unroll
+        for (int s = 0; s < S; s++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                nv[s][c] = *(const float4 *)(e.nw + 16 * (u0 + 64 * s) + 4 * c);
+    }
     uint4 q[RW][P][S];
     uint16_t dh[RW][P][S];
 #pragma unroll
@@ -175,6 +195,29 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
             }
         }
 
+    /* the norm: x <- nw * x at once, and per token the sum of x^2 (the lane's, then the wave's,
+     * left in LDS for the final reduction, whose barrier covers it); s = 1 / sqrt(eps + sum / cols)
+     * multiplies the outputs at the end, W (nw * x) s = W (nw * (x s)): no barrier before the
+     * arithmetic starts, and x and nw are dead once multiplied */
+    float ss[MT];
+    if constexpr (EPI == 1) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; s++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float4 v = xv[m][s][c], g = nv[s][c];
+                    a = __builtin_fmaf(v.x, v.x, a);
+                    a = __builtin_fmaf(v.y, v.y, a);
+                    a = __builtin_fmaf(v.z, v.z, a);
+                    a = __builtin_fmaf(v.w, v.w, a);
+                    xv[m][s][c] = make_float4(g.x * v.x, g.y * v.y, g.z * v.z, g.w * v.w);
+                }
+            ss[m] = q8_wave_sum_dpp(a);
+        }
+    }
     float acc[RW][P][MT];
 #pragma unroll
     for (int r = 0; r < RW; r++)
@@ -203,14 +246,27 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
             for (int m = 0; m < MT; m++) {
                 float v[P];
 #pragma unroll
-                for (int p = 0; p < P; p++)
+                for (int p = 0; p < P; p++) {
                     v[p] = q8_wave_sum_dpp(acc[r][p][m]);
-                if (lane == 0)
-                    y[m * rows + r0 + r] = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
+                    if constexpr (EPI == 1)
+                        v[p] *= 1.0f / sqrtf(e.eps + ss[m] / (float)cols);
+                }
+                if (lane == 0) {
+                    const long i = m * rows + r0 + r;
+                    const float o = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
+                    y[i] = EPI == 2 ? e.res[i] + o : o;
+                }
             }
         return;
     }
     __shared__ float red[NW][RW * P * MT];
+    __shared__ float nsum[EPI == 1 ? NW : 1][MT];
+    if constexpr (EPI == 1) {
+        if (lane == 0)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                nsum[wave][m] = ss[m];
+    }
 #pragma unroll
     for (int r = 0; r < RW; r++)
 #pragma unroll
@@ -232,7 +288,20 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
             for (int k = 1; k < NW; k++)
                 v[p] += red[k][(r * P + p) * MT + m];
         }
-        y[m * rows + r0 + r] = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
+        if constexpr (EPI == 1) {
+            /* the token's sum of x^2 over the waves, in wave order */
+            float tot = nsum[0][m];
+#pragma unroll
+            for (int k = 1; k < NW; k++)
+                tot += nsum[k][m];
+            const float sc = 1.0f / sqrtf(e.eps + tot / (float)cols);
+#pragma unroll
+            for (int p = 0; p < P; p++)
+                v[p] *= sc;
+        }
+        const long i = m * rows + r0 + r;
+        const float o = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
+        y[i] = EPI == 2 ? rv + o : o;
     }
 }
 
@@ -240,7 +309,15 @@ template <int MT, int RW, int S, int NW, int PAIR>
 __global__ __launch_bounds__(64 * NW) void gemv_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
                                                   const float *__restrict__ x, long x_stride, float *__restrict__ y)
 {
-    gemv_body<MT, RW, S, NW, PAIR>(w0, w1, rows, cols, x, x_stride, y, (long)blockIdx.x * RW);
+    gemv_body<MT, RW, S, NW, PAIR, 0>(w0, w1, rows, cols, x, x_stride, y, (long)blockIdx.x * RW, q8_epi{});
+}
+
+/* the same with an epilogue fused (EPI 1: the norm of x first; 2: the residual added to y) */
+template <int MT, int RW, int S, int NW, int PAIR, int EPI>
+__global__ __launch_bounds__(64 * NW) void gemv_ke(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long rows, long cols,
+                                                   const float *__restrict__ x, long x_stride, float *y, q8_epi e)
+{
+    gemv_body<MT, RW, S, NW, PAIR, EPI>(w0, w1, rows, cols, x, x_stride, y, (long)blockIdx.x * RW, e);
 }
 
 /* A round of up to Q8_ROUND_MAX products that share x (the reference's queued products, none
@@ -254,7 +331,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_round(q8_round r, long cols, con
     for (int k = 1; k < Q8_ROUND_MAX; k++)
         if (k < r.n && (long)blockIdx.x >= r.start[k])
             p = k;
-    gemv_body<MT, RW, S, NW, 0>((const uint8_t *)r.w[p], nullptr, r.rows[p], cols, x, x_stride, r.y[p], ((long)blockIdx.x - r.start[p]) * RW);
+    gemv_body<MT, RW, S, NW, 0, 0>((const uint8_t *)r.w[p], nullptr, r.rows[p], cols, x, x_stride, r.y[p], ((long)blockIdx.x - r.start[p]) * RW, q8_epi{});
+}
+
+/* a round with the RMS norm of x fused: every workgroup normalises the x it reads */
+template <int MT, int RW, int S, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_round_norm(q8_round r, long cols, const float *__restrict__ x, long x_stride, q8_epi e)
+{
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < Q8_ROUND_MAX; k++)
+        if (k < r.n && (long)blockIdx.x >= r.start[k])
+            p = k;
+    gemv_body<MT, RW, S, NW, 0, 1>((const uint8_t *)r.w[p], nullptr, r.rows[p], cols, x, x_stride, r.y[p], ((long)blockIdx.x - r.start[p]) * RW, e);
 }
 
 /* Q8_GEMV_CFG = "RW,NW" overrides the decode kernel's rows and waves a workgroup, for tuning sweeps. */
@@ -290,14 +379,12 @@ static bool gemv_go_rw(hipStream_t s, int nw, long kb, const uint8_t *a, const u
     return false;
 }
 
-template <int MT, int PAIR>
-static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y)
+/* The decode kernel's rows a workgroup (rw) and waves (nw) for a shape; kb = cols / 1024 */
+static void gemv_choose(int pair, long rows, long kb, int *rw_out, int *nw_out)
 {
-    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
-    const long kb = cols % 1024 ? 0 : cols / 1024;
     /* measured on the 9B shapes: 8 rows a workgroup (4 for the pair: the same 8 rows of loads a
      * lane), one 1024-column step a wave, so K = 4096 takes 4 waves and K = 12288 takes 12 */
-    int rw = PAIR ? 4 : 8, nw = kb;
+    int rw = pair ? 4 : 8, nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
     /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
@@ -307,6 +394,16 @@ static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, lo
     int erw, enw;
     if (gemv_env(&erw, &enw))
         rw = erw, nw = enw;
+    *rw_out = rw, *nw_out = nw;
+}
+
+template <int MT, int PAIR>
+static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y)
+{
+    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
+    const long kb = cols % 1024 ? 0 : cols / 1024;
+    int rw, nw;
+    gemv_choose(PAIR, rows, kb, &rw, &nw);
     if (kb && rows % rw == 0) {
         bool done = false;
         switch (rw) {
@@ -349,6 +446,112 @@ void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long row
     }
 }
 
+/* ---- the epilogue kernels: the layer shapes' K (S = 1 and NW = 2, 4, 6, 12: K = 2048, 4096,
+ * 6144, 12288) at 2, 4 or 8 rows a workgroup; any other shape runs its epilogue apart */
+template <int MT, int RW, int PAIR, int EPI>
+static bool gemv_epi_rw(hipStream_t s, int nw, long kb, const uint8_t *a, const uint8_t *b, long rows, long cols, const float *x, long xs, float *y,
+                        const q8_epi &e)
+{
+#define K1(S, N)                                                                                                       \
+    if (nw == N && kb == (long)S * N) {                                                                                \
+        Q8_LAUNCH(q8_time_name("gemv_ke", 6, MT, RW, S, N, PAIR, EPI), (gemv_ke<MT, RW, S, N, PAIR, EPI>), dim3((unsigned)(rows / RW)), dim3(64 * N), s, \
+                  a, b, rows, cols, x, xs, y, e);                                                                      \
+        return true;                                                                                                   \
+    }
+    K1(1, 2) K1(1, 4) K1(1, 6)
+    /* K = 12288 (the down matrix): not the pair (no layer has one there), nor 4 tokens at 8 rows
+     * with the norm (both would spill registers) */
+    if constexpr (!PAIR && !(MT == 4 && RW == 8 && EPI == 1)) {
+        K1(1, 12)
+    }
+#undef K1
+    return false;
+}
+
+template <int MT, int PAIR, int EPI>
+static bool gemv_epi_go(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y, const q8_epi &e)
+{
+    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
+    const long kb = cols % 1024 ? 0 : cols / 1024;
+    int rw, nw;
+    gemv_choose(PAIR, rows, kb, &rw, &nw);
+    if (!kb || rows % rw)
+        return false;
+    switch (rw) {
+    case 2: return gemv_epi_rw<MT, 2, PAIR, EPI>(s, nw, kb, a, b, rows, cols, x, xs, y, e);
+    case 4: return gemv_epi_rw<MT, 4, PAIR, EPI>(s, nw, kb, a, b, rows, cols, x, xs, y, e);
+    case 8: return gemv_epi_rw<MT, 8, PAIR, EPI>(s, nw, kb, a, b, rows, cols, x, xs, y, e);
+    default: return false;
+    }
+}
+
+template <int MT>
+static bool gemv_epi_t(hipStream_t s, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, float *y, const q8_epi &e)
+{
+    if (w1)
+        return gemv_epi_go<MT, 1, 1>(s, w0, w1, rows, cols, x, xs, y, e);
+    return e.nw ? gemv_epi_go<MT, 0, 1>(s, w0, w1, rows, cols, x, xs, y, e) : gemv_epi_go<MT, 0, 2>(s, w0, w1, rows, cols, x, xs, y, e);
+}
+
+int q8_launch_gemv_epi(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y,
+                       q8_epi e)
+{
+    if (t < 1 || t > 4 || (e.nw != nullptr) == (e.res != nullptr) || (w1 && e.res))
+        return -1;
+    hipStream_t s = (hipStream_t)stream;
+    bool done;
+    switch (t) {
+    case 1: done = gemv_epi_t<1>(s, w0, w1, rows, cols, x, x_stride, y, e); break;
+    case 2: done = gemv_epi_t<2>(s, w0, w1, rows, cols, x, x_stride, y, e); break;
+    case 3: done = gemv_epi_t<3>(s, w0, w1, rows, cols, x, x_stride, y, e); break;
+    default: done = gemv_epi_t<4>(s, w0, w1, rows, cols, x, x_stride, y, e); break;
+    }
+    return done ? 0 : -1;
+}
+
+/* The RMS norm apart: one workgroup of 256 a token; x^2 summed by each thread over its columns,
+ * then by the wave and across the 4 waves in a fixed order; xn may be x (xs == cols). */
+__global__ __launch_bounds__(256) void rmsnorm_k(const float *x, long xs, long cols, const float *__restrict__ nw, float eps, float *xn)
+{
+    const float *xr = x + (long)blockIdx.x * xs;
+    float *o = xn + (long)blockIdx.x * cols;
+    float a = 0.0f;
+    for (long k = 4 * (long)threadIdx.x; k < cols; k += 1024) {
+        const float4 v = *(const float4 *)(xr + k);
+        a = __builtin_fmaf(v.x, v.x, a);
+        a = __builtin_fmaf(v.y, v.y, a);
+        a = __builtin_fmaf(v.z, v.z, a);
+        a = __builtin_fmaf(v.w, v.w, a);
+    }
+    a = q8_wave_sum_dpp(a);
+    __shared__ float part[4];
+    if ((threadIdx.x & 63) == 0)
+        part[threadIdx.x >> 6] = a;
+    __syncthreads();
+    const float sc = 1.0f / sqrtf(eps + ((part[0] + part[1]) + (part[2] + part[3])) / (float)cols);
+    for (long k = 4 * (long)threadIdx.x; k < cols; k += 1024) {
+        const float4 v = *(const float4 *)(xr + k), g = *(const float4 *)(nw + k);
+        *(float4 *)(o + k) = make_float4(g.x * (v.x * sc), g.y * (v.y * sc), g.z * (v.z * sc), g.w * (v.w * sc));
+    }
+}
+
+void q8_launch_rmsnorm(q8_stream_t stream, const float *x, long x_stride, long t, long cols, const float *nw, float eps, float *xn)
+{
+    rmsnorm_k<<<dim3((unsigned)t), dim3(256), 0, (hipStream_t)stream>>>(x, x_stride, cols, nw, eps, xn);
+}
+
+__global__ __launch_bounds__(256) void add_k(const float *a, const float *b, long n, float *y)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n)
+        y[i] = a[i] + b[i];
+}
+
+void q8_launch_add(q8_stream_t stream, const float *a, const float *b, long n, float *y)
+{
+    add_k<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream>>>(a, b, n, y);
+}
+
 template <int MT, int RW>
 static bool round_go(hipStream_t s, int nw, long kb, const q8_round &r, long cols, const float *x, long xs)
 {
@@ -363,25 +566,75 @@ static bool round_go(hipStream_t s, int nw, long kb, const q8_round &r, long col
     return false;
 }
 
-int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y)
+constexpr int ROUND_RW = 8;
+
+/* the round's table and waves; false when the kernel does not take the shape */
+static bool round_plan(int n, const void *const *w, const long *rows, long cols, long t, float *const *y, q8_round &r, int &nw, long &kb)
 {
-    const long kb = cols % 1024 ? 0 : cols / 1024;
+    kb = cols % 1024 ? 0 : cols / 1024;
     if (n < 1 || n > Q8_ROUND_MAX || t < 1 || t > 4 || !kb)
-        return -1;
-    constexpr int RW = 8;
-    int nw = kb;
+        return false;
+    nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
-    q8_round r = {};
+    r = q8_round{};
     r.n = n;
     for (int i = 0; i < n; i++) {
-        if (rows[i] % RW)
-            return -1;
+        if (rows[i] % ROUND_RW)
+            return false;
         r.w[i] = w[i];
         r.y[i] = y[i];
         r.rows[i] = rows[i];
-        r.start[i + 1] = r.start[i] + rows[i] / RW;
+        r.start[i + 1] = r.start[i] + rows[i] / ROUND_RW;
     }
+    return true;
+}
+
+template <int MT, int RW>
+static bool round_norm_go(hipStream_t s, int nw, long kb, const q8_round &r, long cols, const float *x, long xs, const q8_epi &e)
+{
+#define K1(S, N)                                                                                                       \
+    if (nw == N && kb == (long)S * N) {                                                                                \
+        Q8_LAUNCH(q8_time_name("gemv_round_norm", 4, MT, RW, S, N), (gemv_round_norm<MT, RW, S, N>), dim3((unsigned)r.start[r.n]), dim3(64 * N), s, r, \
+                  cols, x, xs, e);                                                                                     \
+        return true;                                                                                                   \
+    }
+    K1(1, 2) K1(1, 4) K1(1, 6)
+    if constexpr (MT < 4) { /* 4 tokens at K = 12288 would spill registers */
+        K1(1, 12)
+    }
+#undef K1
+    return false;
+}
+
+int q8_launch_gemv_round_epi(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
+                             float *const *y, q8_epi e)
+{
+    q8_round r;
+    int nw;
+    long kb;
+    if (!e.nw || e.res || !round_plan(n, w, rows, cols, t, y, r, nw, kb))
+        return -1;
+    hipStream_t s = (hipStream_t)stream;
+    constexpr int RW = ROUND_RW;
+    bool done = false;
+    switch (t) {
+    case 1: done = round_norm_go<1, RW>(s, nw, kb, r, cols, x, x_stride, e); break;
+    case 2: done = round_norm_go<2, RW>(s, nw, kb, r, cols, x, x_stride, e); break;
+    case 3: done = round_norm_go<3, RW>(s, nw, kb, r, cols, x, x_stride, e); break;
+    default: done = round_norm_go<4, RW>(s, nw, kb, r, cols, x, x_stride, e); break;
+    }
+    return done ? 0 : -1;
+}
+
+int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y)
+{
+    q8_round r;
+    int nw;
+    long kb;
+    if (!round_plan(n, w, rows, cols, t, y, r, nw, kb))
+        return -1;
+    constexpr int RW = ROUND_RW;
     hipStream_t s = (hipStream_t)stream;
     bool done = false;
     switch (t) {

@@ -65,6 +65,9 @@ struct ctx {
     /* scratch for the fused pair when it runs as two products (exact mode, t >= 5): G and U */
     float *scratch = nullptr;
     size_t scratch_cap = 0;
+    /* the epilogues run apart: the normed x, or the product before the residual is added */
+    float *epi = nullptr;
+    size_t epi_cap = 0;
     /* the matrix-core product's K-split partials */
     float *part = nullptr;
     /* the greedy next token's candidates */
@@ -175,6 +178,18 @@ float *reserve_scratch(ctx *c, size_t n)
     return c->scratch;
 }
 
+float *reserve_epi(ctx *c, size_t n)
+{
+    if (n > c->epi_cap) {
+        no_capture(c, "the epilogue's workspace");
+        if (c->epi)
+            c->retired.push_back(c->epi);
+        HIPCHECK(hipMalloc((void **)&c->epi, n * sizeof(float)));
+        c->epi_cap = n;
+    }
+    return c->epi;
+}
+
 void reserve_gemm(ctx *c, long rows, long cols, long t)
 {
     if (!c->part && q8_gemm_part_floats(rows, cols, t) > 0) {
@@ -185,17 +200,25 @@ void reserve_gemm(ctx *c, long rows, long cols, long t)
         fail("the matrix-core product", "its K-split partials exceed the workspace (a planning error)");
 }
 
-/* Y = X W^T for t >= 5 tokens, 64 at a time */
-void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, long xs, long t, float *y)
+/* Y = X W^T for t >= 5 tokens, 64 at a time; res != NULL: Y = res + X W^T (res may be Y), added in
+ * the matrix-core product's store or partial sum */
+void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, long xs, long t, float *y, const float *res = nullptr)
 {
+    const q8_stream_t s = (q8_stream_t)c->stream;
     for (long k = 0; k < t; k += 64) {
         const long n = t - k < 64 ? t - k : 64;
         if (n <= 4) {
-            q8_launch_gemv((q8_stream_t)c->stream, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows);
+            if (!res) {
+                q8_launch_gemv(s, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows);
+            } else if (q8_launch_gemv_epi(s, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows, q8_epi{nullptr, 0.0f, res + k * rows}) != 0) {
+                float *tmp = reserve_epi(c, (size_t)(n * rows));
+                q8_launch_gemv(s, w, nullptr, rows, cols, x + k * xs, xs, n, tmp);
+                q8_launch_add(s, res + k * rows, tmp, n * rows, y + k * rows);
+            }
             continue;
         }
         reserve_gemm(c, rows, cols, n);
-        q8_launch_gemm_mfma((q8_stream_t)c->stream, w, rows, cols, x + k * xs, xs, n, y + k * rows, c->part);
+        q8_launch_gemm_mfma(s, w, rows, cols, x + k * xs, xs, n, y + k * rows, c->part, res ? res + k * rows : nullptr);
     }
 }
 
@@ -241,6 +264,67 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
         q8_launch_swiglu_ew(s, g, g + rows * t, rows * t, y);
     }
     launched("the product");
+}
+
+/* kernel timing for one launch about to be made: the record, or false when timing is off */
+bool kt_begin(ctx *c, int kind, long rows, long cols, long t)
+{
+    if (!c->ktime_on || c->kt.size() >= KT_MAX)
+        return false;
+    const size_t i = c->kt.size();
+    c->kt.push_back(ktrec{kind, rows, cols, t, 0, {0}});
+    q8_time_next(c->kt_events[2 * i], c->kt_events[2 * i + 1], c->kt.back().name, &c->kt.back().grid);
+    return true;
+}
+
+void kt_cancel(ctx *c)
+{
+    q8_time_next(nullptr, nullptr, nullptr, nullptr);
+    c->kt.pop_back();
+}
+
+/* Q8_EPI_APART=1 runs every epilogue as a kernel of its own (the same results: the norm's sum in
+ * its separate kernel's order, the residual the same bits), for comparisons of the two. */
+bool epi_apart()
+{
+    const char *v = getenv("Q8_EPI_APART");
+    return v && v[0] == '1';
+}
+
+/* Y = X W^T (or the fused pair) with an epilogue: the RMS norm of x first (e.nw) or the residual
+ * added to Y (e.res). Fused into the decode kernel where it takes the shape; else the norm apart
+ * into the workspace and then the product, or the residual in the matrix-core product's store, or
+ * the product into the workspace and then the add. */
+void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y, q8_epi e)
+{
+    const q8_stream_t s = (q8_stream_t)c->stream;
+    const bool apart = epi_apart();
+    if (!c->exact && t <= 4 && !apart) {
+        const bool timed = kt_begin(c, RT_K_GEMV + (w1 ? 1 : 0), rows, cols, t);
+        if (q8_launch_gemv_epi(s, w0, w1, rows, cols, x, xs, t, y, e) == 0) {
+            launched("the product and its epilogue");
+            return;
+        }
+        if (timed)
+            kt_cancel(c);
+    }
+    if (e.nw) {
+        float *xn = reserve_epi(c, (size_t)(t * cols));
+        q8_launch_rmsnorm(s, x, xs, t, cols, e.nw, e.eps, xn);
+        launched("the norm");
+        product(c, w0, w1, rows, cols, xn, cols, t, y);
+        return;
+    }
+    if (!c->exact && !w1 && !apart) {
+        kt_begin(c, RT_K_GEMM, rows, cols, t);
+        gemm_tokens(c, w0, rows, cols, x, xs, t, y, e.res);
+        launched("the product and its residual");
+        return;
+    }
+    float *tmp = reserve_epi(c, (size_t)(t * rows));
+    product(c, w0, w1, rows, cols, x, xs, t, tmp);
+    q8_launch_add(s, e.res, tmp, t * rows, y);
+    launched("the residual add");
 }
 
 /* Products sharing x as one launch: true when launched, false when the kernel does not take the
@@ -382,6 +466,8 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipFree(c->scratch));
     if (c->part)
         HIPCHECK(hipFree(c->part));
+    if (c->epi)
+        HIPCHECK(hipFree(c->epi));
     for (void *p : c->retired)
         HIPCHECK(hipFree(p));
     for (auto &e : c->kt_events)
@@ -653,6 +739,95 @@ void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows,
     if (t < 1 || x_stride < cols || x_stride % 4)
         fail("rt_gemv_swiglu_dev", "t >= 1 and x_stride >= cols, a multiple of 4");
     product(c, wg, wu, rows, cols, x, x_stride, t, y);
+}
+
+static void check_rows(const char *fn, long cols, long x_stride, long t)
+{
+    if (t < 1 || x_stride < cols || x_stride % 4)
+        fail(fn, "t >= 1 and x_stride >= cols, a multiple of 4");
+}
+
+void rt_rmsnorm_dev(struct rt *R, const float *x, long x_stride, long t, long cols, const float *nw, float eps, float *xn)
+{
+    ctx *c = get(R, "rt_rmsnorm_dev");
+    check_dev_ptr("rt_rmsnorm_dev", x, "x");
+    check_dev_ptr("rt_rmsnorm_dev", nw, "nw");
+    check_dev_ptr("rt_rmsnorm_dev", xn, "xn");
+    if (cols <= 0 || cols % 4)
+        fail("rt_rmsnorm_dev", "cols must be a positive multiple of 4");
+    check_rows("rt_rmsnorm_dev", cols, x_stride, t);
+    q8_launch_rmsnorm((q8_stream_t)c->stream, x, x_stride, t, cols, nw, eps, xn);
+    launched("the norm");
+}
+
+void rt_gemm_norm_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, const float *nw, float eps, float *y)
+{
+    ctx *c = get(R, "rt_gemm_norm_dev");
+    check_shape(c, "rt_gemm_norm_dev", w, rows, cols);
+    check_dev_ptr("rt_gemm_norm_dev", x, "x");
+    check_dev_ptr("rt_gemm_norm_dev", nw, "nw");
+    check_dev_ptr("rt_gemm_norm_dev", y, "y");
+    check_rows("rt_gemm_norm_dev", cols, x_stride, t);
+    product_epi(c, w, nullptr, rows, cols, x, x_stride, t, y, q8_epi{nw, eps, nullptr});
+}
+
+void rt_gemv_swiglu_norm_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, const float *nw,
+                             float eps, float *y)
+{
+    ctx *c = get(R, "rt_gemv_swiglu_norm_dev");
+    check_shape(c, "rt_gemv_swiglu_norm_dev", wg, rows, cols);
+    check_shape(c, "rt_gemv_swiglu_norm_dev", wu, rows, cols);
+    check_dev_ptr("rt_gemv_swiglu_norm_dev", x, "x");
+    check_dev_ptr("rt_gemv_swiglu_norm_dev", nw, "nw");
+    check_dev_ptr("rt_gemv_swiglu_norm_dev", y, "y");
+    check_rows("rt_gemv_swiglu_norm_dev", cols, x_stride, t);
+    product_epi(c, wg, wu, rows, cols, x, x_stride, t, y, q8_epi{nw, eps, nullptr});
+}
+
+void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
+                            const float *nw, float eps, float *const *y)
+{
+    ctx *c = get(R, "rt_gemv_round_norm_dev");
+    if (n < 1 || n > RT_BATCH || !w || !rows || !y)
+        fail("rt_gemv_round_norm_dev", "needs 1..RT_BATCH (8) products");
+    check_dev_ptr("rt_gemv_round_norm_dev", x, "x");
+    check_dev_ptr("rt_gemv_round_norm_dev", nw, "nw");
+    check_rows("rt_gemv_round_norm_dev", cols, x_stride, t);
+    for (int i = 0; i < n; i++) {
+        check_shape(c, "rt_gemv_round_norm_dev", w[i], rows[i], cols);
+        check_dev_ptr("rt_gemv_round_norm_dev", y[i], "every y");
+    }
+    const q8_stream_t s = (q8_stream_t)c->stream;
+    if (!c->exact && t <= 4 && !epi_apart()) {
+        long total = 0;
+        for (int i = 0; i < n; i++)
+            total += rows[i];
+        const bool timed = kt_begin(c, RT_K_ROUND, total, cols, t);
+        if (q8_launch_gemv_round_epi(s, n, w, rows, cols, x, x_stride, t, y, q8_epi{nw, eps, nullptr}) == 0) {
+            launched("the round and its norm");
+            return;
+        }
+        if (timed)
+            kt_cancel(c);
+    }
+    float *xn = reserve_epi(c, (size_t)(t * cols));
+    q8_launch_rmsnorm(s, x, x_stride, t, cols, nw, eps, xn);
+    launched("the norm");
+    if (!c->exact && t <= 4 && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
+        return;
+    for (int i = 0; i < n; i++)
+        product(c, w[i], nullptr, rows[i], cols, xn, cols, t, y[i]);
+}
+
+void rt_gemm_residual_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, const float *r, float *y)
+{
+    ctx *c = get(R, "rt_gemm_residual_dev");
+    check_shape(c, "rt_gemm_residual_dev", w, rows, cols);
+    check_dev_ptr("rt_gemm_residual_dev", x, "x");
+    check_dev_ptr("rt_gemm_residual_dev", r, "r");
+    check_dev_ptr("rt_gemm_residual_dev", y, "y");
+    check_rows("rt_gemm_residual_dev", cols, x_stride, t);
+    product_epi(c, w, nullptr, rows, cols, x, x_stride, t, y, q8_epi{nullptr, 0.0f, r});
 }
 
 void *rt_dev_alloc(struct rt *R, long bytes)

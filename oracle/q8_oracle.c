@@ -146,6 +146,38 @@ void q8o_gemm_f64(const uint8_t *q8, long rows, long cols, const float *x, long 
     }
 }
 
+void q8o_gemm_f64d(const uint8_t *q8, long rows, long cols, const double *x, long t, double *y)
+{
+    const long nb = cols / BLOCK, row_bytes = nb * BLOCK_BYTES;
+    for (long k = 0; k < t; k++) {
+        const double *xk = x + k * cols;
+        for (long r = 0; r < rows; r++) {
+            const uint8_t *row = q8 + r * row_bytes;
+            double s = 0.0;
+            for (long b = 0; b < nb; b++) {
+                const double d = (double)block_scale(row + b * BLOCK_BYTES);
+                const int8_t *q = (const int8_t *)(row + b * BLOCK_BYTES + 2);
+                for (int i = 0; i < BLOCK; i++)
+                    s += d * (double)q[i] * xk[b * BLOCK + i];
+            }
+            y[k * rows + r] = s;
+        }
+    }
+}
+
+void q8o_rmsnorm_f64(const float *x, long x_stride, long t, long cols, const float *nw, double eps, double *xn)
+{
+    for (long i = 0; i < t; i++) {
+        const float *xi = x + i * x_stride;
+        double ss = 0.0;
+        for (long k = 0; k < cols; k++)
+            ss += (double)xi[k] * (double)xi[k];
+        const double s = 1.0 / sqrt(eps + ss / (double)cols);
+        for (long k = 0; k < cols; k++)
+            xn[i * cols + k] = (double)nw[k] * ((double)xi[k] * s);
+    }
+}
+
 void q8o_swiglu_f64(const double *g, const double *u, long n, double *y)
 {
     for (long i = 0; i < n; i++) {

@@ -29,6 +29,10 @@
  *                    and against numpy's d * q
  *   q8o_next         against the reference's rt_maxv + rt_index_of (oracle/_ref) on random,
  *                    tied, NaN-holding and ragged arrays, and numpy's nanargmax
+ *   q8o_rmsnorm_f64  against the reference's own F32 norm composed from its host rt_sum,
+ *                    rt_s_div, rt_s_add and rt_s_rsqrt (oracle/_ref) within F32 error; a constant
+ *                    vector's closed form; scale invariance and unit RMS at eps = 0
+ *   q8o_gemm_f64d    equal to q8o_gemm_f64 on F32-representable x; linearity in x
  * Nothing here is "parity unpinned". */
 #ifndef Q8_ORACLE_H
 #define Q8_ORACLE_H
@@ -52,6 +56,14 @@ void q8o_gemm_mt(const uint8_t *q8, long rows, long cols, const float *x, long x
 
 /* F64 closed form, Y [t rows]. */
 void q8o_gemm_f64(const uint8_t *q8, long rows, long cols, const float *x, long x_stride, long t, double *y);
+
+/* The same with F64 x (the product of a normed x, which is not an F32 vector). */
+void q8o_gemm_f64d(const uint8_t *q8, long rows, long cols, const double *x, long t, double *y);
+
+/* The RMS norm in F64 (src/apl/qwen35.apl:49, RMS←{⍺×⍵×(RMS_EPS+(+/⍵×⍵)÷≢⍵)*¯0.5}), per token:
+ * xn[i][k] = nw[k] * (x[i][k] * (eps + sum_k x[i][k]^2 / cols)^-0.5); x rows x_stride apart, xn
+ * rows cols apart. */
+void q8o_rmsnorm_f64(const float *x, long x_stride, long t, long cols, const float *nw, double eps, double *xn);
 
 /* SiLU(g) * u in F64 (src/apl/qwen35.apl:38; docs/model.md:29: Sig = 1 / (1 + exp(min(700, -g)))). */
 void q8o_swiglu_f64(const double *g, const double *u, long n, double *y);

@@ -34,6 +34,8 @@ class Oracle:
         L.q8o_gemm.argtypes = [_vp, _l, _l, _vp, _l, _l, _vp]
         L.q8o_gemm_mt.argtypes = [_vp, _l, _l, _vp, _l, _l, _vp, c.c_int]
         L.q8o_gemm_f64.argtypes = [_vp, _l, _l, _vp, _l, _l, _vp]
+        L.q8o_gemm_f64d.argtypes = [_vp, _l, _l, _vp, _l, _vp]
+        L.q8o_rmsnorm_f64.argtypes = [_vp, _l, _l, _l, _vp, c.c_double, _vp]
         L.q8o_swiglu_f64.argtypes = [_vp, _vp, _l, _vp]
         L.q8o_repack_s.argtypes = [_vp, _l, _l, _vp]
         L.q8o_gate_a.argtypes = [_vp]
@@ -63,6 +65,22 @@ class Oracle:
         y = np.empty((t, rows), np.float64)
         self.lib.q8o_gemm_f64(_p(q8), rows, cols, _p(x), cols, t, _p(y))
         return y
+
+    def gemm_f64d(self, q8, rows, cols, x):
+        """F64 closed form with F64 x [t cols]."""
+        x = np.ascontiguousarray(x, np.float64).reshape(-1, cols)
+        y = np.empty((x.shape[0], rows), np.float64)
+        self.lib.q8o_gemm_f64d(_p(q8), rows, cols, _p(x), x.shape[0], _p(y))
+        return y
+
+    def rmsnorm_f64(self, x, nw, eps):
+        """The RMS norm of each row of x [t cols] in F64."""
+        x = np.ascontiguousarray(x, np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        cols = x2.shape[1]
+        out = np.empty(x2.shape, np.float64)
+        self.lib.q8o_rmsnorm_f64(_p(x2), cols, x2.shape[0], cols, _p(np.ascontiguousarray(nw, np.float32)), float(eps), _p(out))
+        return out
 
     def swiglu_f64(self, g, u):
         g = np.ascontiguousarray(g, np.float64)
@@ -142,6 +160,13 @@ class Reference:
         L.rt_index_of.restype = _l
         L.rt_index_of.argtypes = [_vp, _l, c.c_float]
         L.rt_q8_row.argtypes = [_vp, _l, _l, _vp]
+        L.rt_sum.restype = c.c_float
+        L.rt_sum.argtypes = [_vp, _l]
+        for name in ("rt_s_div", "rt_s_add"):
+            getattr(L, name).restype = c.c_float
+            getattr(L, name).argtypes = [c.c_float, c.c_float]
+        L.rt_s_rsqrt.restype = c.c_float
+        L.rt_s_rsqrt.argtypes = [c.c_float]
 
     def gemm(self, q8, rows, cols, x):
         x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
@@ -170,6 +195,18 @@ class Reference:
         z = np.empty(cols + 16, np.float32)
         self.lib.rt_q8_row(_p(fi), cols, row, _p(z))
         return z[:cols]
+
+    def rmsnorm_f32(self, x, nw, eps):
+        """RMS of one row in the reference's F32 host arithmetic: x*x (one rounding, as the host
+        loops' multiply), rt_sum over it, rt_s_div by the length, rt_s_add of eps, rt_s_rsqrt,
+        then nw * (x * s) (src/apl/qwen35.apl:49; src/card/rt.c:106-135)."""
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.size
+        sq = np.zeros((n + 15) // 16 * 16, np.float32)
+        sq[:n] = x * x
+        ss = self.lib.rt_sum(_p(sq), n)
+        s = self.lib.rt_s_rsqrt(self.lib.rt_s_add(np.float32(eps), self.lib.rt_s_div(ss, np.float32(n))))
+        return np.asarray(nw, np.float32) * (x * np.float32(s))
 
     def repack_i(self, q8, rows, cols):
         out = np.empty(rows * cols // 32 * 34, np.uint8)

@@ -222,3 +222,50 @@ def test_row_read_matches_reference(oracle, reference):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         if reference is not None:
             assert np.array_equal(got.view(np.uint32), reference.row(q8, rows, cols, r).view(np.uint32))
+
+
+def test_rmsnorm_f64_matches_reference_f32(oracle, reference):
+    """q8o_rmsnorm_f64 against the reference's own F32 norm, composed from its host rt_sum, rt_s_div,
+    rt_s_add and rt_s_rsqrt (oracle/_ref): F32 error only (<= 1e-6 of the largest output), on
+    lengths that are and are not whole 16-lane blocks, with and without eps."""
+    if reference is None:
+        pytest.skip("oracle/_ref is not built")
+    rng = np.random.default_rng(41)
+    for cols in (1024, 4096, 2064, 100):
+        x = (3 * rng.standard_normal(cols)).astype(np.float32)
+        nw = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+        for eps in (1e-6, 1e-5, 0.0):
+            f64 = oracle.rmsnorm_f64(x[None], nw, eps)[0]
+            r32 = reference.rmsnorm_f32(x, nw, eps)
+            assert np.max(np.abs(f64 - r32)) <= 1e-6 * np.max(np.abs(f64)), (cols, eps)
+
+
+def test_rmsnorm_f64_closed_forms(oracle):
+    """A constant vector's norm in closed form; at eps = 0, scaling x by a power of two changes
+    nothing (exactly) and the normed x has unit RMS; nw multiplies elementwise."""
+    cols = 256
+    ones = np.ones(cols, np.float32)
+    for cval in (2.0, -0.5, 1e-3, 7.25):
+        x = np.full((1, cols), cval, np.float32)
+        got = oracle.rmsnorm_f64(x, ones, 1e-6)[0]
+        want = float(np.float32(cval)) / np.sqrt(1e-6 + float(np.float32(cval)) ** 2)
+        assert np.allclose(got, want, rtol=1e-13, atol=0), cval  # a 256-term F64 sum: ~1e-14
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    a = oracle.rmsnorm_f64(x, ones, 0.0)
+    assert np.array_equal(a, oracle.rmsnorm_f64(x * np.float32(4.0), ones, 0.0))
+    assert np.allclose(np.mean(a * a, axis=1), 1.0, rtol=1e-13, atol=0)
+    nw = rng.standard_normal(cols).astype(np.float32)
+    assert np.array_equal(oracle.rmsnorm_f64(x, nw, 1e-5), nw.astype(np.float64) * oracle.rmsnorm_f64(x, ones, 1e-5))
+
+
+def test_gemm_f64d_is_gemm_f64_on_f32_x(oracle):
+    """The F64-x product equals the F32-x one where x is an F32 vector, and is linear in x."""
+    rows, cols = 48, 256
+    q8, x = synth.case(43, rows, cols, 3)
+    assert np.array_equal(oracle.gemm_f64d(q8, rows, cols, x.astype(np.float64)), oracle.gemm_f64(q8, rows, cols, x))
+    rng = np.random.default_rng(44)
+    x1, x2 = rng.standard_normal((2, cols))
+    lhs = oracle.gemm_f64d(q8, rows, cols, 0.75 * x1 + x2)
+    rhs = 0.75 * oracle.gemm_f64d(q8, rows, cols, x1) + oracle.gemm_f64d(q8, rows, cols, x2)
+    assert np.allclose(lhs, rhs, rtol=1e-12, atol=1e-12)
