@@ -409,10 +409,13 @@ void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *
     const long mt = (t + 15) / 16;
     /* measured on the 9B FFN matrices (12288 x 4096 and 4096 x 12288): 16 waves and 2-pair
      * ranges, every token tile in one workgroup, so the weights are read once */
-    gemm_cfg c = mt == 1 ? CFGS[1] : mt == 2 ? CFGS[7] : mt == 3 ? CFGS[10] : CFGS[12];
-    gemm_cfg e;
+    const gemm_cfg def = mt == 1 ? CFGS[1] : mt == 2 ? CFGS[7] : mt == 3 ? CFGS[10] : CFGS[12];
+    gemm_cfg c = def, e;
     if (env_cfg(&e) && e.mg <= mt)
         c = e;
+    /* a wave owns RT row tiles: RT must divide the matrix's row tiles (the defaults have RT = 1) */
+    if ((rows / 16) % c.rt)
+        c = def;
     const long tiles = (rows + 16L * c.nw * c.rt - 1) / (16L * c.nw * c.rt);
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
     const long groups = (mt + c.mg - 1) / c.mg;
