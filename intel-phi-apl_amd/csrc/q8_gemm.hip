@@ -98,17 +98,6 @@ __device__ __forceinline__ void mfma_block(const bf16x8 (&wb)[RT], const float (
         }
 }
 
-/* x limbs of block b for the MT token tiles */
-template <int MT>
-__device__ __forceinline__ void load_x(uint4 (&xa)[MT][3], const uint4 *xs, long nbp, long b, int lane)
-{
-#pragma unroll
-    for (int m = 0; m < MT; m++)
-#pragma unroll
-        for (int l = 0; l < 3; l++)
-            xa[m][l] = xs[((m * nbp + b) * 3 + l) * 64 + lane];
-}
-
 /* ranges a workgroup streams without draining its loads (one unrolled pipeline) */
 #define GEMM_CHUNK 8
 
