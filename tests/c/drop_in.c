@@ -4,13 +4,19 @@
  * quartet, src/apl/qwen35.apl:93-96); rt_gemm for t tokens. Checks, on synthetic weights:
  *   - exact mode: every y bit-identical to the reference's fold order, computed here in plain C;
  *   - gemm(t)[k] == gemv(x[k]) bit for bit in exact mode (scripts/check.sh:132-149);
- *   - fast mode: within NRMSE 1e-5 of an F64 sum.
+ *   - fast mode: within NRMSE 1e-5 of an F64 sum;
+ *   - include/q8_gguf.h: a GGUF v3 file written here (two Q8_0 tensors and a third tied to the
+ *     first by offset) read and uploaded; the tie shares one handle, and the uploaded matrices give
+ *     the reference fold of the rows written.
  * Prints PASS/FAIL lines; exit 0 only if all pass. Needs the GPU. */
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <unistd.h>
+
+#include "q8_gguf.h"
 #include "q8_rt.h"
 
 static unsigned s = 12345u;
@@ -90,6 +96,49 @@ static double nrmse64(const uint8_t *q8, long rows, long cols, const float *x, c
     return sqrt(num / den);
 }
 
+/* GGUF v3 pieces: little-endian integers, u64-length strings */
+static void put_u32(FILE *f, uint32_t v) { fwrite(&v, 4, 1, f); }
+static void put_u64(FILE *f, uint64_t v) { fwrite(&v, 8, 1, f); }
+static void put_str(FILE *f, const char *s)
+{
+    put_u64(f, strlen(s));
+    fwrite(s, 1, strlen(s), f);
+}
+
+/* A file with one key and tensors "a" (data a), "b" (data b) and "a.tied" (a's offset), all
+ * rows x cols Q8_0; the data start at a multiple of 32. */
+static int write_gguf(const char *path, const uint8_t *a, const uint8_t *b, long rows, long cols)
+{
+    FILE *f = fopen(path, "wb");
+    if (!f)
+        return -1;
+    const uint64_t bytes = (uint64_t)gemv_i_bytes(rows, cols), off_b = (bytes + 31) / 32 * 32;
+    fwrite("GGUF", 1, 4, f);
+    put_u32(f, 3);
+    put_u64(f, 3); /* tensors */
+    put_u64(f, 1); /* keys */
+    put_str(f, "general.architecture");
+    put_u32(f, 8); /* string */
+    put_str(f, "qwen35");
+    const char *names[3] = {"a", "b", "a.tied"};
+    const uint64_t offs[3] = {0, off_b, 0};
+    for (int i = 0; i < 3; i++) {
+        put_str(f, names[i]);
+        put_u32(f, 2);
+        put_u64(f, (uint64_t)cols);
+        put_u64(f, (uint64_t)rows);
+        put_u32(f, 8); /* Q8_0 */
+        put_u64(f, offs[i]);
+    }
+    for (long pos = ftell(f); pos % 32; pos++)
+        fputc(0, f);
+    fwrite(a, 1, bytes, f);
+    for (uint64_t k = bytes; k < off_b; k++)
+        fputc(0, f);
+    fwrite(b, 1, bytes, f);
+    return fclose(f);
+}
+
 static int fails;
 static void check(int ok, const char *what)
 {
@@ -151,6 +200,36 @@ int main(void)
     for (long k = 0; k < T; k++)
         ok &= nrmse64(q8[2], rows, cols, x + k * cols, y + k * rows) <= 1e-5;
     check(ok, "fast rt_gemm(t=6) within NRMSE 1e-5 of F64 per token");
+
+    char path[] = "/tmp/q8_drop_in_XXXXXX";
+    const int fd = mkstemp(path);
+    struct rt_gguf g;
+    char err[512] = "";
+    ok = fd >= 0 && write_gguf(path, q8[0], q8[3], rows, cols) == 0 && rt_gguf_read(&g, path, err, sizeof err) == 0;
+    check(ok, "a GGUF file written here reads (rt_gguf_read)");
+    if (ok) {
+        check(rt_gguf_upload(&R, &g, path, err, sizeof err) == 0 && g.q8_count == 2, "rt_gguf_upload: two distinct matrices");
+        const struct rt_gguf_tensor *ta = rt_gguf_tensor(&g, "a"), *tb = rt_gguf_tensor(&g, "b"), *tt = rt_gguf_tensor(&g, "a.tied");
+        check(ta && tb && tt && ta->w && tt->w == ta->w && tb->w != ta->w && rt_gguf_tensor_at(&g, tb->offset) == tb,
+              "the tie by offset shares one handle; lookups by name and by offset agree");
+        rt_set_exact(&R, 1);
+        same = ta && tb && ta->w && tb->w;
+        for (int k = 0; same && k < 2; k++) {
+            rt_gemv(&R, k ? tb->w : ta->w, rows, cols, x, y);
+            ref_fold(q8[k ? 3 : 0], rows, cols, x, want);
+            same &= memcmp(y, want, sizeof(float) * (size_t)rows) == 0;
+        }
+        check(same, "exact products on the file's matrices == the reference fold of the rows written");
+        rt_set_exact(&R, 0);
+        rt_gguf_release(&R, &g);
+        rt_gguf_free(&g);
+    } else {
+        printf("      %s\n", err);
+    }
+    if (fd >= 0) {
+        close(fd);
+        unlink(path);
+    }
     rt_fini(&R);
     printf("%s\n", fails ? "FAILED" : "ALL PASS");
     return fails != 0;

@@ -474,7 +474,8 @@ def test_fill_generator(rt):
 
 
 def test_c_drop_in_caller(tmp_path):
-    """tests/c/drop_in.c, a C program written against include/q8_rt.h alone, passes its checks."""
+    """tests/c/drop_in.c, a C program written against include/q8_rt.h and include/q8_gguf.h alone,
+    passes its checks."""
     exe = tmp_path / "drop_in"
     lib_dir = os.path.join(ROOT, "intel-phi-apl_amd")
     subprocess.run(["gcc", "-std=gnu11", "-O2", "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "c", "drop_in.c"), "-L", lib_dir,
