@@ -372,11 +372,20 @@ int rt_gguf_upload(struct rt *R, struct rt_gguf *g, const char *path, char *err,
         struct rt_gguf_tensor &t = g->tensors[i];
         if (t.type != RT_GGML_Q8_0)
             continue;
+        /* rows = dim[1]*dim[2]*dim[3], bounded (2^32 rows, 2^28 columns) before anything is
+         * multiplied, so that no size below overflows and the upload gets sane longs */
         uint64_t rows = 1;
-        for (uint32_t d = 1; d < t.n_dims; d++)
+        bool sane = t.dim[0] <= (1ull << 28);
+        for (uint32_t d = 1; d < t.n_dims && sane; d++) {
+            sane = t.dim[d] <= (1ull << 32) && rows * t.dim[d] <= (1ull << 32);
             rows *= t.dim[d];
+        }
         const uint64_t cols = t.n_dims ? t.dim[0] : 0;
-        if (t.n_dims < 2 || rows == 0 || rows % 16 || cols == 0 || cols % 32) {
+        if (!sane) {
+            snprintf(why, sizeof why, "tensor %s: its dimensions are out of range", t.name);
+            goto fail;
+        }
+        if (t.n_dims < 2 || rows == 0 || rows % 16 || cols == 0 || cols % 32 || rows * cols / 32 * 34 != t.bytes) {
             snprintf(why, sizeof why, "tensor %s: %" PRIu64 " rows x %" PRIu64 " columns is not a matrix the products take (rows a multiple of 16, columns of 32)",
                      t.name, rows, cols);
             goto fail;

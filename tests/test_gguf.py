@@ -250,3 +250,24 @@ def test_model_writer_round_trip(q8rt, tmp_path):
             t = g.tensor(name)
             assert t["dim"][:2] == [cols, rows] and t["bytes"] == rows * cols // 32 * 34
             assert np.array_equal(raw[t["offset"]:t["offset"] + t["bytes"]], q8[name])
+
+
+def test_upload_refuses_bad_shapes_before_the_gpu(q8rt, tmp_path):
+    """Q8_0 tensors the products cannot take are refused with their name before anything is
+    uploaded, so no GPU is needed to see it: a 1-D tensor, dimensions whose product overflows 64
+    bits, and more than 2^32 rows (each alone in its file)."""
+    lib = q8rt.load()
+    cases = [("vec", [256], "is not a matrix"), ("huge", [32, 2**40, 2**40], "out of range"), ("tall", [32, 2**33], "out of range")]
+    for name, dims, want in cases:
+        path = tmp_path / f"{name}.gguf"
+        # a header naming the tensor, with no data: the size check must not be what refuses it
+        head = b"GGUF" + struct.pack("<IQQ", 3, 1, 0) + gf.gstr(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", gf.Q8_0, 0)
+        path.write_bytes(head)
+        g = q8rt.GGUF(path)
+        # make the file "complete" as far as the table says, so that the shape is what fails
+        g.h.need = g.h.file_size
+        err = C.create_string_buffer(512)
+        assert lib.rt_gguf_upload(None, C.byref(g.h), os.fsencode(path), err, 512) == -1
+        assert f"tensor {name}:" in err.value.decode() and want in err.value.decode(), err.value.decode()
+        g.close()
