@@ -155,9 +155,6 @@ void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, co
 void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
                          const float *res = nullptr);
 long q8_gemm_part_floats(long rows, long cols, long t);
-/* the kernel's choice for a shape: MG token tiles, RT row tiles a wave, KP pairs of blocks and NW
- * waves a workgroup, ks workgroups along K, cps ranges of KP pairs a workgroup */
-void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *nw, int *ks, int *cps);
 /* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
 void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
 /* z[i] = row rows[i] of w dequantised (q * d, exact), i < n; rows and z device arrays. */

@@ -307,6 +307,156 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
             }
 }
 
+/* One token tile (t <= 16) with x resident in LDS. A workgroup of NW waves owns NW row tiles
+ * (wave w: row tile tile*NW + w) and the split's cps ranges of KP pairs, taken in segments of up
+ * to SC ranges. For a segment, the workgroup first puts x of the segment's blocks (split into
+ * limbs, only the lanes that hold a token's values load them) and its rows' scales into LDS, one
+ * barrier; then each wave streams its weights through two register sets (range ch+1's loads in
+ * flight during range ch's MFMAs) with no further synchronisation. gemm_mfma instead loads x and
+ * the scales for every range, and waits for them and for a barrier before each range's MFMAs.
+ * The sums are gemm_mfma's in the same order, so on the same split the two give the same bits. */
+template <int KP, int NW, int SC>
+__global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                                     float *part, float *y, const float *res)
+{
+    constexpr int BS = 2 * KP * SC;                     /* blocks of a segment */
+    constexpr int XS = 64 * BS;                         /* x lane slots of a segment: 8 values of one token */
+    constexpr int XR = (XS + 64 * NW - 1) / (64 * NW);  /* of them a thread */
+    constexpr int DN = NW * 16 * BS;                    /* scales of a segment */
+    constexpr int DR = (DN + 64 * NW - 1) / (64 * NW);
+    constexpr int DP = BS + 2;                          /* scale row pitch in LDS (halves): an odd dword count, no bank conflicts */
+    __shared__ uint4 xls[BS * 3 * 64];                  /* [block][limb][lane] */
+    __shared__ uint16_t dls[NW * 16 * DP];              /* [row of the workgroup][block] */
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long nb = cols / Q8_BLOCK, np = (nb + 1) / 2;
+    const long tile = blockIdx.x / ks;
+    const int split = (int)(blockIdx.x % ks);
+    const long rt0 = tile * NW + wave;
+    /* a wave past the last row tile reads row tile 0 and contributes nothing */
+    const bool live = rt0 < rows / 16;
+    const int n = lane & 15, kq = lane >> 4;
+    const uint8_t *wq = w + q8s_row_q(live ? rt0 * 16 + n : n, cols) + 16 * kq;
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const long r0 = (long)split * cps, nr = (np + KP - 1) / KP;
+    const int mine = (int)(nr - r0 < cps ? nr - r0 : cps); /* the last split may hold fewer ranges */
+    for (int sb = 0; sb < mine; sb += SC) {
+        const int nc = mine - sb < SC ? mine - sb : SC;
+        const long c00 = (r0 + sb) * KP, b0 = 2 * c00; /* the segment's first pair and block */
+        uint4 q[2][KP];
+        float4 xr[XR][2];
+        uint16_t dr[DR];
+        /* every load of the segment's x and scales, then range 0's weights, all unconditional from
+         * clamped indices (what lies past t or past the last block is zeroed after the loads) */
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < XR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k;
+            const int L = s & 63, bs = s >> 6, tok = L & 15;
+            long b = b0 + (bs < BS ? bs : BS - 1);
+            b = b < nb ? b : nb - 1;
+            const float *px = x + (tok < t ? tok : t - 1) * x_stride + b * Q8_BLOCK + kcol(L >> 4);
+            xr[k][0] = *(const float4 *)px;
+            xr[k][1] = *(const float4 *)(px + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < DR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k;
+            long row = tile * NW * 16 + s / BS;
+            row = row < rows ? row : rows - 1;
+            long b = b0 + s % BS;
+            b = b < nb ? b : nb - 1;
+            dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < KP; p++) {
+            const long c = c00 + p < np ? c00 + p : np - 1;
+            q[0][p] = *(const uint4 *)(wq + 64 * c);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        /* the segment's x limbs and scales into LDS (waits for them, not for the weights) */
+#pragma unroll
+        for (int k = 0; k < XR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k;
+            if (XS % (64 * NW) == 0 || s < XS) {
+                const int L = s & 63, bs = s >> 6, tok = L & 15;
+                const bool in = tok < t && b0 + bs < nb && bs < 2 * KP * nc;
+                const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                uint4 h, m, o;
+                xsplit8(in ? xr[k][0] : z, in ? xr[k][1] : z, h, m, o);
+                xls[(bs * 3 + 0) * 64 + L] = h;
+                xls[(bs * 3 + 1) * 64 + L] = m;
+                xls[(bs * 3 + 2) * 64 + L] = o;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < DR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k;
+            if (DN % (64 * NW) == 0 || s < DN)
+                dls[(s / BS) * DP + s % BS] = dr[k];
+        }
+        __syncthreads();
+        /* the segment's ranges, unrolled whole (a loop back edge would drain the loads in flight):
+         * issue range ch+1 (past the last, range nc-1 again, from L2), then range ch's MFMAs */
+#pragma unroll
+        for (int ch = 0; ch < SC; ch++) {
+            if (ch >= nc)
+                break;
+            __builtin_amdgcn_sched_barrier(0);
+            const int nx = ch + 1 < nc ? ch + 1 : nc - 1;
+#pragma unroll
+            for (int p = 0; p < KP; p++) {
+                long c = c00 + (long)nx * KP + p;
+                c = c < np ? c : np - 1;
+                q[(ch + 1) & 1][p] = *(const uint4 *)(wq + 64 * c);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int p = 0; p < KP; p++) {
+                const long c = c00 + (long)ch * KP + p;
+                const bool ok0 = live && c < np, ok1 = live && 2 * c + 1 < nb; /* block 2c, block 2c+1 */
+                const bool keep = lane < 32 ? ok0 : ok1;
+                const uint4 qq = q[ch & 1][p];
+                /* lanes 0-31 hold block 2c, 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
+                const uint32_t a0 = keep ? qq.x : 0u, a1 = keep ? qq.y : 0u, a2 = keep ? qq.z : 0u, a3 = keep ? qq.w : 0u;
+                const auto s02 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+                const bf16x8 wb[2] = {q8_bf16(s02[0], s13[0]), q8_bf16(s02[1], s13[1])};
+                const int bs = 2 * (ch * KP + p), lr = wave * 16 + n; /* block 2c in the segment, the lane's row in the workgroup */
+                const float d0 = q8_half(dls[lr * DP + bs]), d1 = q8_half(dls[lr * DP + bs + 1]);
+                const float d[2] = {ok0 ? d0 : 0.0f, ok1 ? d1 : 0.0f};
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint4 *xa = xls + (bs + h) * 3 * 64 + lane;
+                    f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[0]), wb[h], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[64]), wb[h], pr, 0, 0, 0);
+                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[128]), wb[h], pr, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[j] = __builtin_fmaf(pr[j], d[h], acc[j]);
+                }
+            }
+        }
+        __syncthreads(); /* every wave done with the segment's LDS before the next segment writes it */
+    }
+    /* lane holds D[token 4*kq + j][row 16*rt0 + n], as in gemm_mfma */
+    if (!live)
+        return;
+    const long tp = (t + 15) / 16 * 16;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const long tok = 4 * kq + j;
+        if (ks == 1) {
+            const long i = tok * rows + rt0 * 16 + n;
+            if (tok < t)
+                y[i] = res ? res[i] + acc[j] : acc[j];
+        } else if (tok < tp) {
+            part[((long)split * tp + tok) * rows + rt0 * 16 + n] = acc[j];
+        }
+    }
+}
+
 /* Y = the sum of the ks partials in split order, one thread an output (the kernel boundary
  * before it makes every split's stores visible), plus the residual when res is given (res may be Y) */
 __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *y, const float *res)
@@ -364,15 +514,20 @@ static bool env_cfg(gemm_cfg *c)
     return false;
 }
 
-/* workgroups of an instance resident on the device at once (occupancy x compute units), asked of
- * the runtime once an instance */
-template <int MG, int RT, int KP, int NW>
-static long gemm_resident()
+/* the x-resident kernel for one token tile: 2-pair ranges, 16 waves, segments of 8 ranges (x
+ * limbs 96 KiB and scales 17 KiB of LDS: one workgroup a CU) */
+#define XRES_KP 2
+#define XRES_NW 16
+#define XRES_SC 8
+
+/* workgroups of a kernel resident on the device at once (occupancy x compute units), asked of the
+ * runtime once a kernel (n caches it) */
+template <typename K>
+static long resident(K kernel, int threads, long &n)
 {
-    static long n = 0;
     if (!n) {
         int per = 0, dev = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, gemm_mfma<MG, RT, KP, NW>, 64 * NW, 0) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per < 1 || cus < 1) {
             fprintf(stderr, "q8_gemm: occupancy query failed\n");
             abort();
@@ -382,8 +537,18 @@ static long gemm_resident()
     return n;
 }
 
-static long cfg_resident(const gemm_cfg &c)
+template <int MG, int RT, int KP, int NW>
+static long gemm_resident()
 {
+    static long n = 0;
+    return resident(gemm_mfma<MG, RT, KP, NW>, 64 * NW, n);
+}
+
+static long cfg_resident(const gemm_cfg &c, bool xres)
+{
+    static long nx = 0;
+    if (xres)
+        return resident(gemm_xres<XRES_KP, XRES_NW, XRES_SC>, 64 * XRES_NW, nx);
 #define GEMM_RES(G, R, P, N)                                                                                           \
     if (c.mg == G && c.rt == R && c.kp == P && c.nw == N)                                                              \
         return gemm_resident<G, R, P, N>();
@@ -393,25 +558,35 @@ static long cfg_resident(const gemm_cfg &c)
     abort();
 }
 
-void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *nw, int *ks, int *cps)
+/* a product's kernel and K split */
+struct gemm_plan {
+    gemm_cfg c;
+    bool xres; /* gemm_xres (one token tile, c = 1, 1, XRES_KP, XRES_NW) rather than gemm_mfma<c> */
+    int ks, cps;
+};
+
+static gemm_plan plan_of(long rows, long cols, long t)
 {
     const long mt = (t + 15) / 16;
     /* measured on the 9B FFN matrices (12288 x 4096 and 4096 x 12288): 16 waves and 2-pair
-     * ranges, every token tile in one workgroup, so the weights are read once */
-    const gemm_cfg def = mt == 1 ? CFGS[1] : mt == 2 ? CFGS[7] : mt == 3 ? CFGS[10] : CFGS[12];
-    gemm_cfg c = def, e;
+     * ranges, every token tile in one workgroup, so the weights are read once; one token tile
+     * keeps x resident */
+    const gemm_cfg def = mt == 1 ? gemm_cfg{1, 1, XRES_KP, XRES_NW} : mt == 2 ? CFGS[7] : mt == 3 ? CFGS[10] : CFGS[12];
+    gemm_plan p = {def, mt == 1, 0, 0};
+    gemm_cfg e;
     if (env_cfg(&e) && e.mg <= mt)
-        c = e;
+        p.c = e, p.xres = false;
     /* a wave owns RT row tiles: RT must divide the matrix's row tiles (the defaults have RT = 1) */
-    if ((rows / 16) % c.rt)
-        c = def;
+    if ((rows / 16) % p.c.rt)
+        p.c = def, p.xres = mt == 1;
+    const gemm_cfg &c = p.c;
     const long tiles = (rows + 16L * c.nw * c.rt - 1) / (16L * c.nw * c.rt);
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
     const long groups = (mt + c.mg - 1) / c.mg;
     const long ranges = (np + c.kp - 1) / c.kp;
     /* the K split: as many splits as fill the device with one resident round of workgroups, each
      * streaming cps ranges; fewer if the partials would not fit the workspace */
-    long split = cfg_resident(c) / (tiles * groups);
+    long split = cfg_resident(c, p.xres) / (tiles * groups);
     const char *v = getenv("Q8_GEMM_KS");
     if (v && atol(v) > 0)
         split = atol(v);
@@ -419,15 +594,15 @@ void q8_gemm_plan(long rows, long cols, long t, int *mg, int *rt, int *kp, int *
     long per = (ranges + split - 1) / split;
     while (per < ranges && (ranges + per - 1) / per * mt * 16 * rows > Q8_GEMM_PART_MAX)
         per++;
-    *mg = c.mg, *rt = c.rt, *kp = c.kp, *nw = c.nw, *cps = (int)per;
-    *ks = (int)((ranges + per - 1) / per);
+    p.cps = (int)per;
+    p.ks = (int)((ranges + per - 1) / per);
+    return p;
 }
 
 long q8_gemm_part_floats(long rows, long cols, long t)
 {
-    int mg, rt, kp, nw, ks, cps;
-    q8_gemm_plan(rows, cols, t, &mg, &rt, &kp, &nw, &ks, &cps);
-    return ks > 1 ? (long)ks * ((t + 15) / 16) * 16 * rows : 0;
+    const gemm_plan p = plan_of(rows, cols, t);
+    return p.ks > 1 ? (long)p.ks * ((t + 15) / 16) * 16 * rows : 0;
 }
 
 template <int MG, int RT, int KP, int NW>
@@ -444,18 +619,28 @@ void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols
                          const float *res)
 {
     hipStream_t s = (hipStream_t)stream;
-    int mg, rt, kp, nw, ks, cps;
-    q8_gemm_plan(rows, cols, t, &mg, &rt, &kp, &nw, &ks, &cps);
+    const gemm_plan p = plan_of(rows, cols, t);
+    const int ks = p.ks, cps = p.cps;
     float *out = ks > 1 ? part : y;
+    const float *r1 = ks > 1 ? nullptr : res;
+    bool done = false;
+    if (p.xres) {
+        const long tiles = (rows + 16L * XRES_NW - 1) / (16L * XRES_NW);
+        Q8_LAUNCH(q8_time_name("gemm_xres", 3, XRES_KP, XRES_NW, XRES_SC), (gemm_xres<XRES_KP, XRES_NW, XRES_SC>), dim3((unsigned)(tiles * ks)),
+                  dim3(64 * XRES_NW), s, (const uint8_t *)w, rows, cols, x, x_stride, t, ks, cps, out, out, r1);
+        done = true;
+    }
 #define GO(G, R, P, N)                                                                                                 \
-    if (mg == G && rt == R && kp == P && nw == N) {                                                                    \
-        gemm_go<G, R, P, N>(s, w, rows, cols, x, x_stride, t, out, part, ks, cps, ks > 1 ? nullptr : res);              \
-        if (ks > 1)                                                                                                    \
-            gemm_sum<<<dim3((unsigned)((t * rows + 255) / 256)), 256, 0, s>>>(part, ks, t, (t + 15) / 16 * 16, rows, y, res); \
-        return;                                                                                                        \
+    if (!done && p.c.mg == G && p.c.rt == R && p.c.kp == P && p.c.nw == N) {                                           \
+        gemm_go<G, R, P, N>(s, w, rows, cols, x, x_stride, t, out, part, ks, cps, r1);                                 \
+        done = true;                                                                                                   \
     }
     GEMM_CFGS(GO)
 #undef GO
-    fprintf(stderr, "q8_gemm: no kernel for MG %d RT %d KP %d NW %d\n", mg, rt, kp, nw);
-    abort();
+    if (!done) {
+        fprintf(stderr, "q8_gemm: no kernel for MG %d RT %d KP %d NW %d\n", p.c.mg, p.c.rt, p.c.kp, p.c.nw);
+        abort();
+    }
+    if (ks > 1)
+        gemm_sum<<<dim3((unsigned)((t * rows + 255) / 256)), 256, 0, s>>>(part, ks, t, (t + 15) / 16 * 16, rows, y, res);
 }
