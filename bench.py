@@ -296,7 +296,8 @@ def deltanet_round(b):
 
 
 def host_pointers(b):
-    """The reference's entry points with host arrays (x copied in, y copied back, one wait a call):
+    """The reference's entry points with host arrays (x staged in pinned memory and copied to HBM by a
+    kernel, y stored by the product into pinned memory, one wait a call):
     rt_gemv on 4096x4096 and the 9B DeltaNet quartet queued with rt_gemv_q and run by rt_gemv_go,
     over rotated weights. The PCIe-inclusive rate, reported beside the HBM-resident one."""
     out = {}
