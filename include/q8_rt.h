@@ -68,8 +68,8 @@ void rt_fini(struct rt *R);
 
 /* ---- products (src/card/rt.h:61-72; rt.c:205-285) */
 
-/* y = W x. x, y host memory: x is copied to HBM, the product runs, y is copied back; returns
- * when y is valid. (rt.c:205-214) */
+/* y = W x. x, y host memory: x is copied to HBM, the product runs and stores y into pinned host
+ * memory, y is copied out; returns when y is valid. (rt.c:205-214) */
 void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
 
 /* Adjacent products: queue up to RT_BATCH, none reading another's result; rt_gemv_go runs them
