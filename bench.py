@@ -628,14 +628,13 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
         m = int(shape.split()[0][1:])
         r_, c_ = (int(v) for v in shape.split()[1].split("x"))
         name = k["kernel"]
-        # the grid rocprof reports is x*y*z threads: match on the name, and on the grid where it is unique
-        keys = [key for key in cnt if key[0] == name]
-        key = next((kk for kk in keys if abs(mean(trace.get(kk, [])) - k["kernel_us"]) / k["kernel_us"] < 0.5), keys[0] if keys else None)
+        # rocprof reports the grid as x*y*z threads, as the bench line does: match on name and grid
+        key = (name, k["grid"])
         c = cnt.get(key, {})
         busy, gui = mean(c.get("SQ_VALU_MFMA_BUSY_CYCLES", [])), mean(c.get("GRBM_GUI_ACTIVE", []))
         mops = mean(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", []))
         util = busy / (gui / xcds * simds) if gui == gui and gui > 0 else float("nan")
-        mg = int(name.split("<")[1].split(",")[0])
+        mg = 1 if name.startswith("gemm_xres") else int(name.split("<")[1].split(",")[0])  # gemm_xres: one token tile
         issued = 2.0 * 3 * (16 * mg * -(-(-(-m // 16)) // mg)) * r_ * c_  # the token tiles the kernel runs: whole groups of MG
         tr = trace.get(key, [])
         rows.append(f"| {shape} | `{name}` | {mean(tr):.2f} | {k['kernel_us']:.2f} | {k['product_us']:.2f} | {k['GFLOPS']:.0f} | "
@@ -651,9 +650,8 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
     text += rows
     text += ["", f"MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). Counted flop = "
              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512; issued = 2 x 3 limbs x the token tiles the kernel runs (whole groups of MG "
-             "tiles of 16: at M = 40, 4 tiles, one of them all padding) x rows x cols. Counters are per (kernel, grid): the "
-             "12288x4096 and 4096x12288 products launch the same grid of the same work (a workgroup: 128 rows x 256 "
-             "columns), and M = 40 and 64 the same grid, so their counter columns are the same averages.", ""]
+             "tiles of 16: at M = 40, 4 tiles, one of them all padding) x rows x cols. Counters are per (kernel, grid): "
+             "products that launch the same kernel on the same grid share one average.", ""]
     open(out, "w").write("\n".join(text))
     print(f"wrote {out}")
 

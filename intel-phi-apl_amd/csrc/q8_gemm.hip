@@ -465,21 +465,21 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
     if (i >= t * rows)
         return;
     const long step = tp * rows;
-    /* eight splits' loads in flight at a time, added in split order */
-    float v = part[i];
-    int s = 1;
-    for (; s + 8 <= ks; s += 8) {
-        float a[8];
+    const float r = res ? res[i] : 0.0f;
+    /* sixteen splits' loads in flight at a time, all issued before the first add (past the last
+     * split the index is clamped and the value not added); added in split order */
+    float v = 0.0f;
+    for (int s0 = 0; s0 < ks; s0 += 16) {
+        float a[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            a[k] = part[(long)(s + k) * step + i];
+        for (int k = 0; k < 16; k++)
+            a[k] = part[(long)(s0 + k < ks ? s0 + k : ks - 1) * step + i];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            v += a[k];
+        for (int k = 0; k < 16; k++)
+            if (s0 + k < ks)
+                v = s0 + k == 0 ? a[0] : v + a[k];
     }
-    for (; s < ks; s++)
-        v += part[(long)s * step + i];
-    y[i] = res ? res[i] + v : v;
+    y[i] = res ? r + v : v;
 }
 
 /* ---------------------------------------------------------------- launchers */
