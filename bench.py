@@ -451,37 +451,40 @@ def layers_2b(b):
 
 
 def cpu_baseline(b, layer, seconds):
-    """The reference's host path on this host's cores over one 9B layer's products (bounded sample)."""
+    """The reference's host path on this host's cores over one 9B layer's products (bounded sample),
+    and, beside it, the same path on configs 1, 4 (M = 16) and 5 (M = 4), a few seconds each."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     threads = min(16, len(os.sched_getaffinity(0)))
     shapes = [("qkv", QKV, HIDDEN), ("out", HIDDEN, HIDDEN), ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN)]
-    # the layer's GGUF rows, drawn again on the GPU from their seeds and copied to the host
-    mats = []
-    seed0 = layer["seed0"]
-    for i, (name, rows, cols) in enumerate(shapes):
-        b.lib.rt_q8_fill_dev(b.R, c.c_void_p(b.staging), rows, cols, seed0 + i, 0, 0.0, 0.02)
+
+    def host_rows(rows, cols, seed, dist=0, mu=0.0, sigma=0.02):
+        """GGUF rows drawn on the GPU from their seed, copied to the host"""
+        b.lib.rt_q8_fill_dev(b.R, c.c_void_p(b.staging), rows, cols, seed, dist, mu, sigma)
         raw = np.empty(q8_bytes(rows, cols), np.uint8)
         b.rt.from_dev(raw, b.staging)
-        mats.append((rows, cols, raw))
+        return raw
+
+    seed0 = layer["seed0"]
+    mats = [(rows, cols, host_rows(rows, cols, seed0 + i)) for i, (name, rows, cols) in enumerate(shapes)]
     rng = np.random.default_rng(0)
-    xs = {cols: rng.standard_normal(cols, dtype=np.float32) for _, _, cols in shapes}
     nbytes = sum(alg_bytes(r, k, 1) for _, r, k in shapes)
     try:
         from oracle_ffi import Reference
 
         ref = Reference()
         kind = "reference"
-        forms = []
-        for rows, cols, raw in mats:
-            fi = ref.repack_i(raw, rows, cols)
-            forms.append((rows, cols, fi, np.empty(rows, np.float32)))
         team = ref.lib.ref_team_create(threads)
         if not team:
             raise OSError("team")
 
-        def one():
-            for rows, cols, fi, y in forms:
-                ref.lib.ref_team_gemv_i(c.c_void_p(team), c.c_void_p(fi.ctypes.data), rows, cols, c.c_void_p(xs[cols].ctypes.data),
+        def prepare(rows, cols, raw):
+            return ref.repack_i(raw, rows, cols)
+
+        def product(form, rows, cols, x, t, y):
+            if t == 1:
+                ref.lib.ref_team_gemv_i(c.c_void_p(team), c.c_void_p(form.ctypes.data), rows, cols, c.c_void_p(x.ctypes.data), c.c_void_p(y.ctypes.data))
+            else:
+                ref.lib.ref_team_gemm_i(c.c_void_p(team), c.c_void_p(form.ctypes.data), rows, cols, c.c_void_p(x.ctypes.data), t,
                                         c.c_void_p(y.ctypes.data))
         done = lambda: ref.lib.ref_team_destroy(c.c_void_p(team))  # noqa: E731
     except (FileNotFoundError, OSError):
@@ -489,25 +492,55 @@ def cpu_baseline(b, layer, seconds):
 
         orc = Oracle()
         kind = "port"
-        outs = [np.empty(r, np.float32) for r, _, _ in mats]
 
-        def one():
-            for (rows, cols, raw), y in zip(mats, outs):
-                orc.lib.q8o_gemm_mt(c.c_void_p(raw.ctypes.data), rows, cols, c.c_void_p(xs[cols].ctypes.data), cols, 1, c.c_void_p(y.ctypes.data), threads)
+        def prepare(rows, cols, raw):
+            return raw
+
+        def product(form, rows, cols, x, t, y):
+            orc.lib.q8o_gemm_mt(c.c_void_p(form.ctypes.data), rows, cols, c.c_void_p(x.ctypes.data), cols, t, c.c_void_p(y.ctypes.data), threads)
         done = lambda: None  # noqa: E731
-    one()  # warm-up, dropped (src/bench/gemv_bench.c:113-125)
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 200):
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    done()
-    med = statistics.median(times)
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"one 9B decode layer (QKV 6144x4096, out 4096x4096, gate and up 12288x4096, down 4096x12288: {nbytes} B), "
-                      f"median of {len(times)} passes after one warm-up, {threads} threads pinned to this host's CPUs",
-            "ms_per_layer": round(1e3 * med, 2), "host_cpus": os.cpu_count()}
+
+    def median_time(run, budget, at_least=3, at_most=200):
+        run()  # warm-up, dropped (src/bench/gemv_bench.c:113-125)
+        times = []
+        t_end = time.perf_counter() + budget
+        while len(times) < at_least or (time.perf_counter() < t_end and len(times) < at_most):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    def job(rows, cols, raw, t):
+        x = rng.standard_normal((t, cols), dtype=np.float32)
+        return (prepare(rows, cols, raw), rows, cols, x, t, np.empty((t, rows), np.float32))
+
+    try:
+        layer_jobs = [job(rows, cols, raw, 1) for rows, cols, raw in mats]
+        med, n = median_time(lambda: [product(*j) for j in layer_jobs], seconds)
+        out = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+               "sample": f"one 9B decode layer (QKV 6144x4096, out 4096x4096, gate and up 12288x4096, down 4096x12288: {nbytes} B), "
+                         f"median of {n} passes after one warm-up, {threads} threads pinned to this host's CPUs",
+               "ms_per_layer": round(1e3 * med, 2), "host_cpus": os.cpu_count()}
+        configs = {}
+        # config 1: the 4096x4096 GEMV (seed 0 rows, as the parity fixtures)
+        j1 = job(HIDDEN, HIDDEN, host_rows(HIDDEN, HIDDEN, 0), 1)
+        med, n = median_time(lambda: product(*j1), 2.0)
+        configs["gemv_4096x4096"] = {"ms": round(1e3 * med, 3), "GB/s": round(alg_bytes(HIDDEN, HIDDEN, 1) / med / 1e9, 3), "passes": n}
+        # config 4: the prompt GEMM, M = 16, gate/up shape
+        j4 = job(FFN, HIDDEN, host_rows(FFN, HIDDEN, 7), 16)
+        med, n = median_time(lambda: product(*j4), 4.0, at_least=2)
+        configs["gemm_m16_12288x4096"] = {"ms": round(1e3 * med, 2), "GFLOPS": round(2.0 * 16 * FFN * HIDDEN / med / 1e9, 2), "passes": n}
+        # config 5: verify at M = 4, gate and up then down, heavy-tailed scales
+        kw = dict(dist=1, mu=float(np.log(0.002)), sigma=1.0)
+        j5 = [job(FFN, HIDDEN, host_rows(FFN, HIDDEN, 8, **kw), 4), job(FFN, HIDDEN, host_rows(FFN, HIDDEN, 9, **kw), 4),
+              job(HIDDEN, FFN, host_rows(HIDDEN, FFN, 10, **kw), 4)]
+        med, n = median_time(lambda: [product(*j) for j in j5], 4.0, at_least=2)
+        v_bytes = alg_bytes(FFN, HIDDEN, 4, pair=True) + alg_bytes(HIDDEN, FFN, 4)
+        configs["verify_m4_gate_up_down"] = {"ms": round(1e3 * med, 2), "GB/s": round(v_bytes / med / 1e9, 3), "passes": n}
+        out["configs"] = configs
+    finally:
+        done()
+    return out
 
 
 CALIB_BYTES = 1 << 30
