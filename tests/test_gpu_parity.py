@@ -500,6 +500,34 @@ def test_host_pointer_entry_points(rt):
             rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+def test_host_pointer_staging_grows_and_refreshes(rt):
+    """The host-pointer products store y into pinned staging that grows with the call: a sequence of
+    growing shapes and token counts (up to 70 tokens, two matrix-core launches into one y), the
+    reference-order kernel, and a repeat with a new x, each equal bit for bit to the device path."""
+    rng = np.random.default_rng(41)
+    cases = [(256, 1024, 1), (4096, 1024, 3), (1024, 4096, 16), (8192, 1024, 70), (512, 2048, 4)]
+    for rows, cols, t in cases:
+        q8 = synth.q8_rows(rng, rows, cols)
+        w = rt.upload(q8, rows, cols)
+        try:
+            for exact in (False, True) if t <= 4 else (False,):
+                old = rt.set_exact(exact)
+                try:
+                    for rep in range(2):
+                        x = synth.x_f32(rng, t, cols)
+                        Y = np.full((t, rows), np.nan, np.float32)
+                        if t == 1:
+                            rt.gemv(w, rows, cols, x[0], Y[0])
+                        else:
+                            rt.gemm(w, rows, cols, x, t, Y)
+                        say("host staging", rows, cols, t, "exact" if exact else "fast", rep)
+                        assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, q8, rows, cols, x, exact=exact, w=w).view(np.uint32))
+                finally:
+                    rt.set_exact(old)
+        finally:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
 def test_edge_scales(rt, oracle):
     """Zero scales give +0; subnormal, largest-finite and negative binary16 scales; q at -128..127 (the
     GGUF byte range, wider than the generator's)."""
