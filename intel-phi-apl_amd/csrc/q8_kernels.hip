@@ -380,11 +380,12 @@ static bool gemv_go_rw(hipStream_t s, int nw, long kb, const uint8_t *a, const u
 }
 
 /* The decode kernel's rows a workgroup (rw) and waves (nw) for a shape; kb = cols / 1024 */
-static void gemv_choose(int pair, long rows, long kb, int *rw_out, int *nw_out)
+static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *nw_out)
 {
     /* measured on the 9B shapes: 8 rows a workgroup (4 for the pair: the same 8 rows of loads a
-     * lane), one 1024-column step a wave, so K = 4096 takes 4 waves and K = 12288 takes 12 */
-    int rw = pair ? 4 : 8, nw = (int)kb;
+     * lane; 8 for the pair at 2 and 3 tokens, 5 % faster there and 7 % slower at 1 and 4), one
+     * 1024-column step a wave, so K = 4096 takes 4 waves and K = 12288 takes 12 */
+    int rw = pair ? (mt == 2 || mt == 3 ? 8 : 4) : 8, nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
     /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
@@ -403,7 +404,7 @@ static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, lo
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
     const long kb = cols % 1024 ? 0 : cols / 1024;
     int rw, nw;
-    gemv_choose(PAIR, rows, kb, &rw, &nw);
+    gemv_choose(PAIR, MT, rows, kb, &rw, &nw);
     if (kb && rows % rw == 0) {
         bool done = false;
         switch (rw) {
@@ -474,7 +475,7 @@ static bool gemv_epi_go(hipStream_t s, const void *w0, const void *w1, long rows
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
     const long kb = cols % 1024 ? 0 : cols / 1024;
     int rw, nw;
-    gemv_choose(PAIR, rows, kb, &rw, &nw);
+    gemv_choose(PAIR, 1, rows, kb, &rw, &nw); /* the fused-epilogue instances: as measured at one token */
     if (!kb || rows % rw)
         return false;
     switch (rw) {
