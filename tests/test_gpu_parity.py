@@ -528,6 +528,43 @@ def test_host_pointer_staging_grows_and_refreshes(rt):
             rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+INVARIANT_CASES = [(256, 1024, 1), (512, 2048, 3), (1024, 4096, 16), (768, 1056, 9), (512, 4096, 40)]
+
+
+@pytest.mark.parametrize("rows,cols,t", INVARIANT_CASES)
+def test_one_hot_x_reads_a_column(rt, rows, cols, t):
+    """x = e_j (token k's j differs per token: block edges, the last column) gives column j of d*q
+    exactly on the fast kernels: every other term is an exact zero, and x = 1 has no lower limbs on
+    the matrix cores. Decode (t <= 4), x-resident (5..16, 1056 columns: half a final pair) and
+    streaming (t > 16) kernels."""
+    rng = np.random.default_rng(rows + cols + t)
+    q8 = synth.q8_rows(rng, rows, cols)
+    q, d = synth.split(q8, rows, cols)
+    cols_hot = [(31 + 32 * 5 * k + 7 * k) % cols for k in range(t)]
+    cols_hot[-1] = cols - 1
+    x = np.zeros((t, cols), np.float32)
+    for k, j in enumerate(cols_hot):
+        x[k, j] = 1.0
+    got = gpu_gemm(rt, q8, rows, cols, x)
+    want = np.stack([d[:, j // 32].astype(np.float32) * q[:, j].astype(np.float32) for j in cols_hot])
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,cols,t", INVARIANT_CASES)
+def test_permuting_row_groups_permutes_y(rt, rows, cols, t):
+    """Reordering the 16-row groups of W reorders Y the same way, bit for bit: no kernel's per-row
+    arithmetic depends on where the row sits."""
+    rng = np.random.default_rng(7 * rows + cols + t)
+    q8 = synth.q8_rows(rng, rows, cols)
+    x = synth.x_f32(rng, t, cols)
+    perm = rng.permutation(rows // 16)
+    rows_of = (perm[:, None] * 16 + np.arange(16)[None, :]).reshape(-1)
+    q8p = q8.reshape(rows, -1)[rows_of].reshape(-1)
+    y = gpu_gemm(rt, q8, rows, cols, x)
+    yp = gpu_gemm(rt, q8p, rows, cols, x)
+    assert np.array_equal(yp.view(np.uint32), y[:, rows_of].view(np.uint32))
+
+
 def test_edge_scales(rt, oracle):
     """Zero scales give +0; subnormal, largest-finite and negative binary16 scales; q at -128..127 (the
     GGUF byte range, wider than the generator's)."""
