@@ -21,6 +21,8 @@
  *               (split into limbs on the way into LDS), its rows' scales (into LDS) and every weight
  *               of every wave, with the next range's loads in flight during this one's wait and
  *               MFMAs. With K split over ks workgroups, each writes a partial;
+ *   gemm_xres   the same for one token tile (t <= 16), with the split's x limbs and scales put in
+ *               LDS once, so the weights stream with no per-range wait or barrier;
  *   gemm_sum    adds the ks partials in split order: the same order every run, deterministic. */
 #include <hip/hip_runtime.h>
 
