@@ -321,35 +321,38 @@ def test_fused_pair_many_tokens(rt, oracle):
 
 
 def test_graph_replays_match_eager(rt):
-    """A recorded sequence (decode products, the fused pair and a K-split matrix-core product, which
-    resets its own counters) replayed three times, with eager work between the replays, gives the
-    eager result bit for bit every time."""
+    """A recorded sequence (decode products, the fused pair, and K-split matrix-core products at 16
+    tokens (x-resident, 32 splits) and 40 (streaming), whose partials every run writes before it
+    sums them) replayed three times, with eager work between the replays, gives the eager result
+    bit for bit every time."""
     rng = np.random.default_rng(8)
-    rows, cols, t = 2048, 4096, 16
+    rows, cols, t, t2 = 2048, 4096, 16, 40
     mats = [synth.q8_rows(rng, rows, cols) for _ in range(3)]
-    x = synth.x_f32(rng, t, cols)
+    x = synth.x_f32(rng, t2, cols)
     ws = [rt.upload(m, rows, cols) for m in mats]
     with Dev(rt) as d:
         dx = d.put(x)
-        y1, y2, y3 = d.empty(4 * rows), d.empty(4 * 2 * rows), d.empty(4 * t * rows)
+        y1, y2, y3, y4 = d.empty(4 * rows), d.empty(4 * 2 * rows), d.empty(4 * t * rows), d.empty(4 * t2 * rows)
         yz = d.empty(4 * t * rows)
+        outs = ((y1, rows), (y2, 2 * rows), (y3, t * rows), (y4, t2 * rows))
 
         def seq():
             rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[0]), rows, cols, c.c_void_p(dx), cols, 1, c.c_void_p(y1))
             rt.lib.rt_gemv_swiglu_dev(rt.R, c.c_void_p(ws[1]), c.c_void_p(ws[2]), rows, cols, c.c_void_p(dx), cols, 2, c.c_void_p(y2))
             rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[2]), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(y3))
+            rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[1]), rows, cols, c.c_void_p(dx), cols, t2, c.c_void_p(y4))
 
         seq()
-        want = [d.get(p, n, np.float32) for p, n in ((y1, rows), (y2, 2 * rows), (y3, t * rows))]
+        want = [d.get(p, n, np.float32) for p, n in outs]
         rt.lib.rt_graph_begin(rt.R)
         seq()
         g = rt.lib.rt_graph_end(rt.R)
         try:
             for rep in range(3):
-                for p, n in ((y1, rows), (y2, 2 * rows), (y3, t * rows)):
+                for p, n in outs:
                     rt.to_dev(p, np.zeros(n, np.float32))
                 rt.lib.rt_graph_launch(rt.R, c.c_void_p(g))
-                got = [d.get(p, n, np.float32) for p, n in ((y1, rows), (y2, 2 * rows), (y3, t * rows))]
+                got = [d.get(p, n, np.float32) for p, n in outs]
                 for a, b in zip(got, want):
                     assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep}"
                 # eager work between replays: another K-split product on the same workspace
