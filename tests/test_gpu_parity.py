@@ -531,6 +531,38 @@ def test_host_pointer_staging_grows_and_refreshes(rt):
             rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+def random_cases(n=28, seed=2024):
+    """Seeded shapes across every product path: rows a multiple of 16 (one tile to 1536 rows), cols a
+    multiple of 32 (odd block counts included), t from 1 to 70 (decode, x-resident, streaming, more
+    than 64 tokens), normal or heavy-tailed scales."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        rows = 16 * int(rng.integers(1, 97))
+        cols = 32 * int(rng.integers(1, 129))
+        t = int(rng.choice([1, 2, 3, 4, 5, 7, 9, 12, 16, 17, 23, 32, 33, 40, 47, 64, 65, 70]))
+        out.append((i, rows, cols, t, "lognormal" if i % 3 == 2 else "normal"))
+    return out
+
+
+@pytest.mark.parametrize("case", random_cases(), ids=lambda c: f"{c[1]}x{c[2]}t{c[3]}")
+def test_random_shapes_every_path(rt, oracle, case):
+    """The fast kernels against the F64 closed form at the parity bar, and the reference-order kernel
+    against the oracle bit for bit, on seeded random shapes."""
+    i, rows, cols, t, dist = case
+    q8, x = synth.case(9000 + i, rows, cols, t, dist)
+    say("random", rows, cols, t, dist)
+    w = rt.upload(q8, rows, cols)
+    try:
+        got = gpu_gemm(rt, q8, rows, cols, x, w=w)
+        assert_parity(got, oracle.gemm_f64(q8, rows, cols, x), f"{rows}x{cols} t={t} {dist}")
+        if rows * cols * t <= 1 << 24:
+            ex = gpu_gemm(rt, q8, rows, cols, x, exact=True, w=w)
+            assert np.array_equal(ex.view(np.uint32), oracle.gemm(q8, rows, cols, x).view(np.uint32))
+    finally:
+        rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
 INVARIANT_CASES = [(256, 1024, 1), (512, 2048, 3), (1024, 4096, 16), (768, 1056, 9), (512, 4096, 40)]
 
 
