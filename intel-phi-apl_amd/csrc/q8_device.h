@@ -170,6 +170,8 @@ void q8_launch_fill(q8_stream_t stream, void *dst, long rows, long cols, uint64_
 void q8_launch_fill_f32(q8_stream_t stream, float *dst, long n, uint64_t seed);
 /* dst = src, n16 16-byte words, both device. */
 void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16);
+/* *flag = seq once the kernels before it on the stream are done; flag in pinned host memory. */
+void q8_launch_flag(q8_stream_t stream, unsigned *flag, unsigned seq);
 /* The primitive conversions of the product kernels, lane by lane (the reference's gate 2.1
  * s8 and f16 sets, src/gate/upconv_kernel.c:18-57). */
 void q8_launch_prims(q8_stream_t stream, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h,

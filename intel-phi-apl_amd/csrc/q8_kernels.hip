@@ -905,6 +905,19 @@ void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16)
     copy16<<<dim3((unsigned)((n16 + 255) / 256)), 256, 0, (hipStream_t)stream>>>((uint4 *)dst, (const uint4 *)src, n16);
 }
 
+/* *flag = seq, stored by lane 0 with release order at system scope: the host sees it after every
+ * store of the kernels before this one on the stream (each kernel's end writes back its stores). */
+__global__ void set_flag(unsigned *flag, unsigned seq)
+{
+    if (threadIdx.x == 0)
+        __hip_atomic_store(flag + threadIdx.x, seq + threadIdx.x, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+void q8_launch_flag(q8_stream_t stream, unsigned *flag, unsigned seq)
+{
+    set_flag<<<1, 64, 0, (hipStream_t)stream>>>(flag, seq);
+}
+
 /* ---------------------------------------------------------------- primitive gates */
 
 /* o8[i] = fma(x8[i], s8(q[i]), c8[i]) through the product kernels' byte convert (four bytes
