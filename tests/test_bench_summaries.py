@@ -1,0 +1,93 @@
+"""The benchmark's profile writers (bench.summarize, bench.summarize_gemm) on small synthetic runs in
+rocprofv3's CSV layout: each product is matched to its own kernel and grid (two products that share
+a kernel name on different grids stay apart), trace averages and counter scaling come out as
+computed by hand, and the matrix-core table counts the x-resident kernel as one token tile."""
+import csv
+import json
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def _csv(path, fields, rows):
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        w.writerows(rows)
+
+
+def _trace(path, launches):
+    """launches: (kernel name, grid threads, [durations in us])"""
+    rows, t = [], 1000
+    for name, grid, durs in launches:
+        for d in durs:
+            rows.append({"Kernel_Name": f"void {name}(unsigned char const*, long)", "Grid_Size_X": grid, "Grid_Size_Y": 1, "Grid_Size_Z": 1,
+                         "Start_Timestamp": t, "End_Timestamp": t + int(round(d * 1000))})
+            t += 100000
+    _csv(path, ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp", "End_Timestamp"], rows)
+
+
+def _counters(path, values):
+    """values: (kernel name, grid, counter, [values])"""
+    rows = [{"Kernel_Name": f"void {n}(float const*)", "Grid_Size": g, "Counter_Name": cn, "Counter_Value": v} for n, g, cn, vs in values for v in vs]
+    _csv(path, ["Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"], rows)
+
+
+def test_decode_summary_matches_kernel_and_grid(tmp_path):
+    run = tmp_path / "run"
+    k = "gemv_k<1, 8, 1, 4, 0>"
+    kernels_9b = {"gemv 4096x4096 t1": {"kernel": k, "grid": 131072, "us": 5.0, "alg_bytes": 17858560},
+                  "gemv 6144x4096 t1": {"kernel": k, "grid": 196608, "us": 6.5, "alg_bytes": 26779648}}
+    line = {"metric": "m", "kernels_9b": kernels_9b, "device": "gfx950", "config": {"workload": "w"}, "ms_per_step": 1.5,
+            "eager_ms_per_step": 1.5,
+            "roofline": {"kernel": f"{k} (gemv 6144x4096, t=1, grid 196608)", "bytes_per_launch": 26779648}}
+    os.makedirs(run)
+    (run / "prof_stats.log").write_text("noise\n" + json.dumps(line) + "\n")
+    _trace(str(run / "prof_stats" / "run_kernel_trace.csv"), [(k, 131072, [5.0, 5.2]), (k, 196608, [7.0, 7.4, 7.2])])
+    _csv(str(run / "prof_stats" / "run_kernel_stats.csv"), ["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"],
+         [{"Name": f"void {k}(float const*)", "Calls": 5, "AverageNs": 6360.0, "MinNs": 5000, "MaxNs": 7400, "Percentage": 100.0}])
+    ck = ("copy16", bench.CALIB_BYTES // 16)
+    # the yardstick reads half its bytes on FETCH_SIZE and all on WRITE_SIZE: scales 2 and 1
+    _counters(str(run / "prof_fetch" / "run_counter_collection.csv"),
+              [(ck[0], ck[1], "FETCH_SIZE", [bench.CALIB_BYTES / 2048.0]), (k, 131072, "FETCH_SIZE", [8800.0, 8800.0]), (k, 196608, "FETCH_SIZE", [13100.0])])
+    _counters(str(run / "prof_write" / "run_counter_collection.csv"),
+              [(ck[0], ck[1], "WRITE_SIZE", [bench.CALIB_BYTES / 1024.0]), (k, 131072, "WRITE_SIZE", [16.0]), (k, 196608, "WRITE_SIZE", [24.0])])
+    out = tmp_path / "decode.md"
+    bench.summarize(str(run), out=str(out))
+    text = out.read_text()
+    blob = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    a, b = blob[f"{k} grid 131072"], blob[f"{k} grid 196608"]
+    assert a["trace_us"] == pytest.approx(5.1) and b["trace_us"] == pytest.approx(7.2)
+    assert a["traffic"] == round(1024 * (8800.0 * 2 + 16.0)) and b["traffic"] == round(1024 * (13100.0 * 2 + 24.0))
+    assert "Dominant kernel" in text and "7.2 us per launch" in text
+
+
+def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path):
+    run = tmp_path / "run"
+    xr, mf = "gemm_xres<2, 16, 8>", "gemm_mfma<3, 1, 2, 16>"
+    shapes = {"M16 12288x4096": (xr, 245760, 18.0, 12288, 4096, 16), "M16 4096x12288": (xr, 262144, 19.0, 4096, 12288, 16),
+              "M40 12288x4096": (mf, 245760, 27.0, 12288, 4096, 40)}
+    line = {"prompt_gemm": {s: {"kernel": n, "grid": g, "kernel_us": us, "product_us": us + 1, "GFLOPS": 1.0} for s, (n, g, us, _, _, _) in shapes.items()}}
+    os.makedirs(run)
+    (run / "gprof_stats.log").write_text(json.dumps(line) + "\n")
+    _trace(str(run / "gprof_stats" / "run_kernel_trace.csv"), [(xr, 245760, [17.0, 17.4]), (xr, 262144, [18.5]), (mf, 245760, [26.0, 28.0])])
+    # issued bf16 MFMA flop = 2 x 3 limbs x the token tiles run x rows x cols; the counter counts 512 flop a MOP
+    mops = {(n, g): 2.0 * 3 * (16 * (1 if n == xr else 3)) * r * c / 512 for n, g, _, r, c, _ in shapes.values()}
+    _counters(str(run / "gprof_fetch" / "run_counter_collection.csv"), [(n, g, "FETCH_SIZE", [30000.0]) for (n, g) in mops])
+    vals = []
+    for (n, g), m in mops.items():
+        vals += [(n, g, "SQ_INSTS_VALU_MFMA_MOPS_BF16", [m]), (n, g, "SQ_VALU_MFMA_BUSY_CYCLES", [1024.0]), (n, g, "GRBM_GUI_ACTIVE", [8.0 * 10])]
+    _counters(str(run / "gprof_mfma" / "run_counter_collection.csv"), vals)
+    out = tmp_path / "gemm.md"
+    bench.summarize_gemm(str(run), out=str(out))
+    rows = {l.split("|")[1].strip(): [c.strip() for c in l.split("|")[2:-1]] for l in out.read_text().splitlines() if l.startswith("| M")}
+    assert rows["M16 12288x4096"][1] == "17.20" and rows["M16 4096x12288"][1] == "18.50" and rows["M40 12288x4096"][1] == "27.00"
+    for s in shapes:
+        assert rows[s][-1] == "1.000", s  # counted / issued: one token tile for gemm_xres, three for gemm_mfma<3, ...>
+        assert rows[s][-2] == "10.0", s   # MFMA busy: 1024 cycles over (80 / 8 XCDs x 1024 SIMDs)
