@@ -130,9 +130,9 @@ void check_dev_ptr(const char *fn, const void *p, const char *what)
     }
 }
 
-void grow_pinned(float **p, size_t *cap_unused, size_t n)
+/* *p = a pinned host buffer of n floats (the old one freed: no call is in flight when it grows) */
+void grow_pinned(float **p, size_t n)
 {
-    (void)cap_unused;
     if (*p)
         HIPCHECK(hipHostFree(*p));
     HIPCHECK(hipHostMalloc((void **)p, n * sizeof(float), hipHostMallocDefault));
@@ -142,7 +142,7 @@ void reserve_staging(ctx *c, size_t nx, size_t ny)
 {
     if (nx > c->x_cap) {
         size_t n = nx + nx / 2 + 4096;
-        grow_pinned(&c->hx, nullptr, n);
+        grow_pinned(&c->hx, n);
         if (c->dx)
             HIPCHECK(hipFree(c->dx));
         HIPCHECK(hipMalloc((void **)&c->dx, n * sizeof(float)));
@@ -150,7 +150,7 @@ void reserve_staging(ctx *c, size_t nx, size_t ny)
     }
     if (ny > c->y_cap) {
         size_t n = ny + ny / 2 + 4096;
-        grow_pinned(&c->hy, nullptr, n);
+        grow_pinned(&c->hy, n);
         c->y_cap = n;
     }
 }
