@@ -230,3 +230,45 @@ def test_epilogues_apart_switch(rt, oracle):
     ref = oracle.gemm_f64d(q8, rows, cols, oracle.rmsnorm_f64(x, nw, EPS))
     assert_parity(out[True][1], ref, "norm product apart")
     assert_parity(out[False][1], ref, "norm product fused")
+
+
+def _random_epilogue_cases(n=16, seed=77):
+    """seeded shapes: rows a multiple of 16, cols a multiple of 32 (odd block counts, K of the fused
+    kernels and others), t across decode and matrix-core counts"""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        rows = 16 * int(rng.integers(1, 81))
+        cols = int(rng.choice([2048, 4096, 12288])) if i % 4 == 0 else 32 * int(rng.integers(1, 97))
+        t = int(rng.choice([1, 2, 3, 4, 5, 9, 16, 23]))
+        out.append((i, rows, cols, t))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_epilogue_cases(), ids=lambda c: f"{c[1]}x{c[2]}t{c[3]}")
+def test_epilogues_random_shapes(rt, oracle, case):
+    """The norm before and the residual after a product on seeded random shapes, whichever route the
+    shape takes (fused into the decode or matrix-core kernel, or apart): the norm product at the
+    parity bar against F64, the residual bit for bit against the product plus one F32 add, in place
+    too."""
+    i, rows, cols, t = case
+    say(f"random epilogues {rows}x{cols} t={t}")
+    q8, x = synth.case(5000 + i, rows, cols, t)
+    nw = _vec(6000 + i, cols)
+    r = np.random.default_rng(7000 + i).standard_normal((t, rows)).astype(np.float32)
+    w = rt.upload(q8, rows, cols)
+    try:
+        with Dev(rt) as d:
+            dx, dn, dr, dy = d.put(x), d.put(nw), d.put(r), d.empty(4 * t * rows)
+            rt.lib.rt_gemm_norm_dev(rt.R, c.c_void_p(w), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(dn), EPS, c.c_void_p(dy))
+            yn = d.get(dy, (t, rows), np.float32)
+            rt.lib.rt_gemm_residual_dev(rt.R, c.c_void_p(w), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(dr), c.c_void_p(dy))
+            yr = d.get(dy, (t, rows), np.float32)
+            rt.lib.rt_gemm_residual_dev(rt.R, c.c_void_p(w), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(dr), c.c_void_p(dr))
+            inplace = d.get(dr, (t, rows), np.float32)
+        plain = gpu_gemm(rt, q8, rows, cols, x, w=w)
+    finally:
+        rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+    assert_parity(yn, oracle.gemm_f64d(q8, rows, cols, oracle.rmsnorm_f64(x, nw, EPS)), f"norm product {rows}x{cols} t={t}")
+    assert np.array_equal(yr.view(np.uint32), (r + plain).view(np.uint32))
+    assert np.array_equal(inplace.view(np.uint32), yr.view(np.uint32))
