@@ -269,3 +269,58 @@ def test_gemm_f64d_is_gemm_f64_on_f32_x(oracle):
     lhs = oracle.gemm_f64d(q8, rows, cols, 0.75 * x1 + x2)
     rhs = 0.75 * oracle.gemm_f64d(q8, rows, cols, x1) + oracle.gemm_f64d(q8, rows, cols, x2)
     assert np.allclose(lhs, rhs, rtol=1e-12, atol=1e-12)
+
+
+def swiglu_violations(f):
+    """The facts the mathematics fixes for the reference's FFN activation, Sig = {1 / (1 + exp(min(700,
+    -g)))} and SiLU = {g x Sig g}, times u (src/apl/qwen35.apl:37-38, 124-126), checked on f(g, u) (F64
+    arrays in, F64 out). Returns the names of the facts f breaks; the oracle must break none."""
+    bad = []
+    rng = np.random.default_rng(51)
+    g = rng.uniform(-30.0, 30.0, 4000)
+    u = rng.uniform(-4.0, 4.0, 4000)
+    ones = np.ones_like(g)
+    if not np.all(f(np.zeros(8), np.linspace(-3, 3, 8)) == 0.0):
+        bad.append("SiLU(0) u = 0")
+    # SiLU(g) - SiLU(-g) = g (1 / (1 + e^-g) + 1 / (1 + e^g)) = g: pins the exponent's sign
+    if not np.allclose(f(g, ones) - f(-g, ones), g, rtol=1e-12, atol=1e-12):
+        bad.append("SiLU(g) - SiLU(-g) = g")
+    # Sig(ln 3) = 1 / (1 + 1/3) = 3/4 exactly in the reals
+    l3 = np.log(3.0)
+    if not np.allclose(f(np.full(6, l3), u[:6]), 0.75 * l3 * u[:6], rtol=1e-14, atol=0):
+        bad.append("SiLU(ln 3) u = 3/4 ln 3 u")
+    # a large positive g: Sig -> 1, the output is g u
+    big = np.array([40.0, 60.0, 100.0, 700.0, 1e4])
+    if not np.allclose(f(big, np.full(5, -1.5)), -1.5 * big, rtol=1e-15, atol=0):
+        bad.append("SiLU(g) u = g u for large g")
+    # through the 700 clamp: -800 and -1e6 give exp(700), finite, so the output is a finite ~0
+    neg = np.array([-800.0, -1e6, -709.0, -701.0])
+    y = f(neg, np.full(4, 2.0))
+    if not (np.all(np.isfinite(y)) and np.all(np.abs(y) < 1e-290)):
+        bad.append("finite ~0 through the 700 clamp")
+    # linear in u
+    if not np.allclose(f(g, 3.0 * u), 3.0 * f(g, u), rtol=1e-14, atol=1e-300):
+        bad.append("linear in u")
+    # the textbook logistic at a few points: Sig(g) = (1 + tanh(g / 2)) / 2
+    pts = np.array([-5.0, -1.0, 0.5, 2.0, 7.0])
+    if not np.allclose(f(pts, ones[:5]), pts * (1.0 + np.tanh(pts / 2.0)) / 2.0, rtol=1e-14, atol=1e-300):
+        bad.append("Sig(g) = (1 + tanh(g / 2)) / 2")
+    return bad
+
+
+def test_swiglu_f64_pinned(oracle):
+    """q8o_swiglu_f64 meets every fact of swiglu_violations; the mistakes one could plant in it (the
+    exponent's sign flipped, the x u dropped, the clamp's min turned into max, the logistic's 1 +
+    left out) each break at least one."""
+    assert swiglu_violations(oracle.swiglu_f64) == []
+
+    planted = {
+        "exp(+g)": lambda g, u: g / (1.0 + np.exp(np.minimum(700.0, g))) * u,
+        "x u dropped": lambda g, u: g / (1.0 + np.exp(np.minimum(700.0, -g))),
+        "max for min": lambda g, u: g / (1.0 + np.exp(np.maximum(700.0, -g))) * u,
+        "no 1 +": lambda g, u: g / np.exp(np.minimum(700.0, -g)) * u,
+        "u for g": lambda g, u: u / (1.0 + np.exp(np.minimum(700.0, -g))) * u,
+    }
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        for name, f in planted.items():
+            assert swiglu_violations(f), f"the planted mistake '{name}' passes every check"
