@@ -157,7 +157,8 @@ void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const lon
 /* Y = R + X W^T (after W_OUT and W_DOWN); r [t rows] may be y, the residual stream updated in place. */
 void rt_gemm_residual_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, const float *r, float *y);
 /* z[i*cols ..] = row rows[i] of w dequantised, i < n (rows: device longs, each < the matrix's
- * rows; z device). The embedding read of a batch of tokens. An addition. */
+ * rows; z device). The embedding read of a batch of tokens. An addition. The indices are device
+ * data the host does not see: one outside [0, rows) reads nothing and gives a row of NaN. */
 void rt_q8_rows_dev(struct rt *R, const void *w, long cols, const long *rows, long n, float *z);
 /* *idx (device) = the greedy next token over a[0..n) (device): the lowest i whose bits equal the
  * fmaxf fold of a, as the host's rt_maxv then rt_index_of give it (src/card/rt.c:137-165) for

@@ -157,8 +157,9 @@ void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols
 long q8_gemm_part_floats(long rows, long cols, long t);
 /* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
 void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
-/* z[i] = row rows[i] of w dequantised (q * d, exact), i < n; rows and z device arrays. */
-void q8_launch_rows(q8_stream_t stream, const void *w, long cols, const long *rows, long n, float *z);
+/* z[i] = row rows[i] of w dequantised (q * d, exact), i < n; rows and z device arrays; an index
+ * outside [0, nrows) gives a row of NaN. */
+void q8_launch_rows(q8_stream_t stream, const void *w, long cols, long nrows, const long *rows, long n, float *z);
 /* *out = the lowest i with a[i] bit-equal to the fmaxf fold of a[0..n); cm, ci hold
  * q8_argmax_chunks(n) candidates. */
 long q8_argmax_chunks(long n);

@@ -727,8 +727,11 @@ void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, 
 /* ---------------------------------------------------------------- rows and the greedy next token */
 
 /* z[i][k] = q * d of row rows[i] (src/card/rt.c:484-501: q converted, times the block scale, one
- * rounding; exact, since d*q has at most 19 significant bits). One thread per 4 columns. */
-__global__ __launch_bounds__(256) void q8_rows_k(const uint8_t *__restrict__ w, long cols, const long *__restrict__ rows, long n, float *__restrict__ z)
+ * rounding; exact, since d*q has at most 19 significant bits). One thread per 4 columns. An index
+ * outside [0, nrows) reads nothing and gives a row of NaN: the indices are device data, which the
+ * host cannot check before the launch. */
+__global__ __launch_bounds__(256) void q8_rows_k(const uint8_t *__restrict__ w, long cols, long nrows, const long *__restrict__ rows, long n,
+                                                 float *__restrict__ z)
 {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const long per = cols / 4;
@@ -736,15 +739,20 @@ __global__ __launch_bounds__(256) void q8_rows_k(const uint8_t *__restrict__ w, 
         return;
     const long k = i / per, c4 = 4 * (i % per);
     const long r = rows[k];
+    if (r < 0 || r >= nrows) {
+        const float nan = __builtin_nanf("");
+        *(float4 *)(z + k * cols + c4) = make_float4(nan, nan, nan, nan);
+        return;
+    }
     const uint32_t q = *(const uint32_t *)(w + q8s_row_q(r, cols) + c4);
     const float d = q8_half(((const uint16_t *)(w + q8s_row_d(r, cols)))[c4 / Q8_BLOCK]);
     *(float4 *)(z + k * cols + c4) = make_float4(q8_s8(q, 0) * d, q8_s8(q, 1) * d, q8_s8(q, 2) * d, q8_s8(q, 3) * d);
 }
 
-void q8_launch_rows(q8_stream_t stream, const void *w, long cols, const long *rows, long n, float *z)
+void q8_launch_rows(q8_stream_t stream, const void *w, long cols, long nrows, const long *rows, long n, float *z)
 {
     const long m = n * (cols / 4);
-    q8_rows_k<<<dim3((unsigned)((m + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)w, cols, rows, n, z);
+    q8_rows_k<<<dim3((unsigned)((m + 255) / 256)), 256, 0, (hipStream_t)stream>>>((const uint8_t *)w, cols, nrows, rows, n, z);
 }
 
 /* The greedy next token of the reference's Next = {w index-of max/w} (src/apl/qwen35.apl:161; the

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <errno.h>
+#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -29,16 +30,39 @@
         }                                                                                                              \
     } while (0)
 
-static void fail(const char *fn, const char *why)
+/* A caller's mistake (a bad shape, an unregistered handle, a misaligned address): the reason on
+ * stderr, then abort(), as the reference's entry points fail, before anything is launched.
+ * Q8_ABORT_EXIT=n (1..125) ends the process with _exit(n) instead, for test harnesses that check
+ * the message of an expected failure in a child process without a SIGABRT. */
+[[noreturn]] static void failv(const char *fn, const char *fmt, va_list ap)
 {
-    fprintf(stderr, "q8_rt: %s: %s\n", fn, why);
+    fprintf(stderr, "q8_rt: %s: ", fn);
+    vfprintf(stderr, fmt, ap);
+    fputc('\n', stderr);
+    fflush(stderr);
+    const char *v = getenv("Q8_ABORT_EXIT");
+    const int code = v ? atoi(v) : 0;
+    if (code >= 1 && code <= 125)
+        _exit(code);
     abort();
 }
 
+[[noreturn]] __attribute__((format(printf, 2, 3))) static void failf(const char *fn, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    failv(fn, fmt, ap);
+}
+
+[[noreturn]] static void fail(const char *fn, const char *why) { failf(fn, "%s", why); }
+
 namespace {
 
+/* a registered weight handle: its shape, and whether the library allocated it (rt_q8_upload and
+ * the like) or only registered a caller's buffer (rt_q8_repack_dev) */
 struct matrix {
     long rows, cols;
+    bool owned;
 };
 
 struct ktrec {
@@ -106,28 +130,28 @@ ctx *get(struct rt *R, const char *fn)
     return (ctx *)R->chain;
 }
 
+/* w must be a handle the registry holds (from an upload, or a buffer rt_q8_repack_dev wrote), used
+ * as its own shape or a prefix of its whole 16-row groups: anything else (a host pointer left by an
+ * engine still on its own repack, an address inside a matrix, a freed handle) aborts here, before
+ * a kernel could read it */
 void check_shape(ctx *c, const char *fn, const void *w, long rows, long cols)
 {
     if (!w)
         fail(fn, "w is NULL");
-    if (rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK) {
-        fprintf(stderr, "q8_rt: %s: rows %ld must be a positive multiple of 16 and cols %ld of 32\n", fn, rows, cols);
-        abort();
-    }
+    if (rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK)
+        failf(fn, "rows %ld must be a positive multiple of 16 and cols %ld of 32", rows, cols);
     auto it = c->weights.find(w);
-    if (it != c->weights.end() && (it->second.cols != cols || rows > it->second.rows)) {
-        fprintf(stderr, "q8_rt: %s: w was uploaded as %ld x %ld, used as %ld x %ld (only a prefix of whole 16-row groups may be used)\n", fn,
-                it->second.rows, it->second.cols, rows, cols);
-        abort();
-    }
+    if (it == c->weights.end())
+        failf(fn, "w %p is not a weight handle (rt_q8_upload, rt_q8_upload_fd, rt_q8_upload_packed, rt_gguf_upload or rt_q8_repack_dev make them)", w);
+    if (it->second.cols != cols || rows > it->second.rows)
+        failf(fn, "w was uploaded as %ld x %ld, used as %ld x %ld (only a prefix of whole 16-row groups may be used)", it->second.rows, it->second.cols,
+              rows, cols);
 }
 
 void check_dev_ptr(const char *fn, const void *p, const char *what)
 {
-    if (!p || ((uintptr_t)p & 15)) {
-        fprintf(stderr, "q8_rt: %s: %s must be a 16-byte aligned device address\n", fn, what);
-        abort();
-    }
+    if (!p || ((uintptr_t)p & 15))
+        failf(fn, "%s must be a 16-byte aligned device address", what);
 }
 
 /* *p = a pinned host buffer of n floats (the old one freed: no call is in flight when it grows) */
@@ -161,10 +185,8 @@ void no_capture(ctx *c, const char *what)
 {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     HIPCHECK(hipStreamIsCapturing(c->stream, &st));
-    if (st != hipStreamCaptureStatusNone) {
-        fprintf(stderr, "q8_rt: %s must grow while a graph is being recorded: run a product of this size once before rt_graph_begin\n", what);
-        abort();
-    }
+    if (st != hipStreamCaptureStatusNone)
+        failf(what, "must grow while a graph is being recorded: run a product of this size once before rt_graph_begin");
 }
 
 float *reserve_scratch(ctx *c, size_t n)
@@ -228,7 +250,7 @@ void launched(const char *what)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         fprintf(stderr, "q8_rt: launch of %s failed: %s\n", what, hipGetErrorString(e));
-        abort();
+        abort(); /* a HIP failure, not a caller's mistake */
     }
 }
 
@@ -484,7 +506,8 @@ void rt_fini(struct rt *R)
     ctx *c = (ctx *)R->chain;
     HIPCHECK(hipStreamSynchronize(c->stream));
     for (auto &kv : c->weights)
-        HIPCHECK(hipFree((void *)kv.first));
+        if (kv.second.owned)
+            HIPCHECK(hipFree((void *)kv.first));
     if (c->hx)
         HIPCHECK(hipHostFree(c->hx));
     if (c->hy)
@@ -593,9 +616,9 @@ void gemv_i_repack(const uint8_t *q8, long rows, long cols, void *out)
     }
 }
 
-static const void *register_matrix(ctx *c, void *dev, long rows, long cols)
+static const void *register_matrix(ctx *c, void *dev, long rows, long cols, bool owned = true)
 {
-    c->weights[dev] = matrix{rows, cols};
+    c->weights[dev] = matrix{rows, cols, owned};
     return dev;
 }
 
@@ -721,6 +744,8 @@ void rt_q8_free(struct rt *R, const void *w)
     auto it = c->weights.find(w);
     if (it == c->weights.end())
         fail("rt_q8_free", "w is not a handle from rt_q8_upload");
+    if (!it->second.owned)
+        fail("rt_q8_free", "w is a buffer of the caller's that rt_q8_repack_dev registered: free it with rt_dev_free");
     HIPCHECK(hipStreamSynchronize(c->stream));
     HIPCHECK(hipFree((void *)w));
     c->weights.erase(it);
@@ -873,6 +898,12 @@ void *rt_dev_alloc(struct rt *R, long bytes)
 void rt_dev_free(struct rt *R, void *p)
 {
     ctx *c = get(R, "rt_dev_free");
+    auto it = c->weights.find(p);
+    if (it != c->weights.end()) {
+        if (it->second.owned)
+            fail("rt_dev_free", "p is a weight handle the library allocated: free it with rt_q8_free");
+        c->weights.erase(it); /* a buffer rt_q8_repack_dev registered stops being a handle */
+    }
     HIPCHECK(hipStreamSynchronize(c->stream));
     HIPCHECK(hipFree(p));
 }
@@ -907,8 +938,12 @@ void rt_q8_repack_dev(struct rt *R, const void *q8_dev, long rows, long cols, vo
     ctx *c = get(R, "rt_q8_repack_dev");
     if (!q8_dev || !out_dev || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK || ((uintptr_t)out_dev & 31) || ((uintptr_t)q8_dev & 1))
         fail("rt_q8_repack_dev", "needs rows a positive multiple of 16, cols of 32, out 32-byte aligned");
+    auto it = c->weights.find(out_dev);
+    if (it != c->weights.end() && it->second.owned)
+        fail("rt_q8_repack_dev", "out_dev is a weight handle the library allocated");
     q8_launch_repack((q8_stream_t)c->stream, q8_dev, rows, cols, out_dev);
     launched("the repack");
+    register_matrix(c, out_dev, rows, cols, false);
 }
 
 void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed)
@@ -936,7 +971,7 @@ void rt_q8_row(const void *w, long cols, long row, float *z)
     ((long *)c->hx)[0] = row, ((long *)c->hx)[1] = 0;
     q8_launch_copy((q8_stream_t)c->stream, dr, c->hx, 1);
     launched("the copy of the row index");
-    q8_launch_rows((q8_stream_t)c->stream, w, cols, dr, 1, c->hy);
+    q8_launch_rows((q8_stream_t)c->stream, w, cols, it->second.rows, dr, 1, c->hy);
     launched("the row read");
     wait_done(c);
     memcpy(z, c->hy, sizeof(float) * (size_t)cols);
@@ -951,7 +986,7 @@ void rt_q8_rows_dev(struct rt *R, const void *w, long cols, const long *rows, lo
     if (cols != it->second.cols || n < 1 || !rows)
         fail("rt_q8_rows_dev", "cols must be the matrix's and n >= 1");
     check_dev_ptr("rt_q8_rows_dev", z, "z");
-    q8_launch_rows((q8_stream_t)c->stream, w, cols, rows, n, z);
+    q8_launch_rows((q8_stream_t)c->stream, w, cols, it->second.rows, rows, n, z);
     launched("the row gather");
 }
 

@@ -68,3 +68,29 @@ def test_c_caller_compiles_and_links(tmp_path):
                         os.path.join(ROOT, "tests", "c", "drop_in.c"), "-L", os.path.join(ROOT, "intel-phi-apl_amd"), "-lq8rt",
                         "-Wl,-rpath," + os.path.join(ROOT, "intel-phi-apl_amd"), "-lm", "-o", str(exe)], capture_output=True, text=True)
     assert p.returncode == 0, p.stderr
+
+
+REF_CARD = "/root/reference/src/card"
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(REF_CARD, "rt.h")), reason="the reference's sources are not here (only in the build container)")
+def test_reference_header_identical(tmp_path):
+    """A caller compiled against the reference's own src/card/rt.h links against libq8rt.so with
+    link-time type checking: every product entry point's parameter and return types (rt.h:38-39,
+    61-72, 85) are the reference's (-Werror=lto-type-mismatch), and struct rt's size, field offsets
+    and RT_BATCH (rt.h:19-26, 66) equal this library's."""
+    inc, lib = os.path.join(ROOT, "include"), os.path.join(ROOT, "intel-phi-apl_amd")
+    objs = []
+    for src, flag in (("ref_abi_ref.c", REF_CARD), ("ref_abi_own.c", inc)):
+        o = tmp_path / (src + ".o")
+        p = subprocess.run(["gcc", "-std=gnu11", "-O1", "-flto", "-Wall", "-Werror", "-I", flag, "-c", os.path.join(ROOT, "tests", "c", src), "-o", str(o)],
+                           capture_output=True, text=True)
+        assert p.returncode == 0, p.stderr
+        objs.append(str(o))
+    exe = tmp_path / "ref_abi"
+    p = subprocess.run(["gcc", "-O1", "-flto", "-Werror=lto-type-mismatch", *objs, "-L", lib, "-lq8rt", "-Wl,-rpath," + lib, "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert p.returncode == 0, p.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "layout identical" in r.stdout

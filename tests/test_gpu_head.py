@@ -1,0 +1,143 @@
+"""GPU parity at the output head and the draft head, and the batch deviation of the fast kernels.
+
+  - Logits (src/apl/qwen35.apl:158-160): the 151936 x 4096 output head at 1, 3 and 16 tokens, the
+    fast kernels against the F64 closed form at the parity bar, the reference-order kernel against
+    the oracle's F32 order bit for bit (1 and 3 tokens);
+  - DraftLogits (qwen35.apl:170-172): the first 32768 rows of the same handle equal the first
+    32768 outputs of the full product bit for bit;
+  - the reference keeps gemm(t)[k] == gemv(x[k]) bit for bit (src/card/gemm.h:7). Here the
+    reference-order kernel keeps it, the decode kernel (t <= 4) keeps it, and the matrix-core
+    product (t >= 5, any K split) does not: its outputs differ from the one-token product's by
+    the F32 rounding of another summation order, bounded here by the parity bar.
+"""
+import ctypes as c
+import os
+
+import numpy as np
+import pytest
+
+from parity import assert_parity, metrics
+
+pytestmark = pytest.mark.gpu
+
+VOCAB, HIDDEN, DRAFT = 151936, 4096, 32768
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+class Handle:
+    """A Q8_0 matrix drawn on the device (rt_q8_fill_dev), repacked into a buffer that becomes a
+    registered handle (rt_q8_repack_dev); its GGUF rows also on the host, for the oracle."""
+
+    def __init__(self, rt, rows, cols, seed, dist=0, mu=0.0, sigma=0.02):
+        self.rt, self.rows, self.cols = rt, rows, cols
+        nbytes = rows * cols // 32 * 34
+        src = rt.alloc(nbytes)
+        rt.lib.rt_q8_fill_dev(rt.R, c.c_void_p(src), rows, cols, seed, dist, c.c_float(mu), c.c_float(sigma))
+        self.q8 = np.empty(nbytes, np.uint8)
+        rt.from_dev(self.q8, src)
+        self.w = rt.alloc(nbytes)
+        rt.lib.rt_q8_repack_dev(rt.R, c.c_void_p(src), rows, cols, c.c_void_p(self.w))
+        rt.sync()
+        rt.free(src)
+
+    def product(self, x, rows=None, exact=False):
+        """Y [t rows] = X W[:rows]^T through rt_gemm_dev."""
+        rt = self.rt
+        rows = rows or self.rows
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.cols)
+        t = x.shape[0]
+        old = rt.set_exact(exact)
+        dx, dy = rt.alloc(x.nbytes), rt.alloc(4 * t * rows)
+        try:
+            rt.to_dev(dx, x)
+            rt.lib.rt_gemm_dev(rt.R, c.c_void_p(self.w), rows, self.cols, c.c_void_p(dx), self.cols, t, c.c_void_p(dy))
+            y = np.empty((t, rows), np.float32)
+            rt.from_dev(y, dy)
+        finally:
+            rt.free(dx)
+            rt.free(dy)
+            rt.set_exact(old)
+        return y
+
+    def close(self):
+        self.rt.free(self.w)
+
+
+@pytest.fixture(scope="module")
+def head(rt):
+    say("head: drawing 151936 x 4096 Q8_0 on the device")
+    h = Handle(rt, VOCAB, HIDDEN, seed=151936)
+    yield h
+    h.close()
+
+
+@pytest.mark.parametrize("t", [1, 3, 16])
+def test_output_head_parity(rt, oracle, head, t):
+    """The 151936 x 4096 head: fast kernels at the parity bar against F64, every output finite."""
+    x = np.random.default_rng(1000 + t).standard_normal((t, HIDDEN), dtype=np.float32)
+    say(f"head t={t}: GPU product")
+    y = head.product(x)
+    say(f"head t={t}: F64 oracle")
+    want = oracle.gemm_f64(head.q8, VOCAB, HIDDEN, x)
+    m = assert_parity(y, want, f"head t={t}")
+    say(f"head t={t}:", m)
+
+
+@pytest.mark.parametrize("t", [1, 3])
+def test_output_head_reference_order(rt, oracle, head, t):
+    """The reference-order kernel on the head equals the oracle's F32 order bit for bit."""
+    x = np.random.default_rng(2000 + t).standard_normal((t, HIDDEN), dtype=np.float32)
+    y = head.product(x, exact=True)
+    want = oracle.gemm(head.q8, VOCAB, HIDDEN, x, threads=8)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [1, 3])
+def test_draft_head_is_prefix(rt, oracle, head, t):
+    """rt_gemm_dev with rows = 32768 on the 151936-row handle: the first 32768 outputs of the full
+    product, bit for bit, in the fast and the reference-order kernels; and at the parity bar."""
+    x = np.random.default_rng(3000 + t).standard_normal((t, HIDDEN), dtype=np.float32)
+    for exact in (False, True):
+        full = head.product(x, exact=exact)
+        draft = head.product(x, rows=DRAFT, exact=exact)
+        assert np.array_equal(draft.view(np.uint32), full[:, :DRAFT].view(np.uint32)), f"exact={exact}"
+    want = oracle.gemm_f64(head.q8[: DRAFT * HIDDEN // 32 * 34], DRAFT, HIDDEN, x)
+    assert_parity(draft, want, f"draft t={t}")
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (4096, 12288)])
+def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
+    """gemm(t)[k] against gemv(x[k]) (src/card/gemm.h:7): bit for bit in the reference-order kernel at
+    every t and in the decode kernel at t <= 4; at t >= 5 (the matrix cores) and at every K split
+    tried (1, 3 and the planner's), within the parity bar of the one-token product and of F64."""
+    h = Handle(rt, rows, cols, seed=rows + cols)
+    try:
+        X = np.random.default_rng(rows ^ cols).standard_normal((40, cols), dtype=np.float32)
+        one = np.concatenate([h.product(X[k]) for k in range(40)])
+        one_exact = np.concatenate([h.product(X[k], exact=True) for k in range(8)])
+        f64 = oracle.gemm_f64(h.q8, rows, cols, X)
+        assert_parity(one, f64, "gemv per token")
+        for t in (2, 3, 4):
+            y = h.product(X[:t])
+            assert np.array_equal(y.view(np.uint32), one[:t].view(np.uint32)), f"decode kernel t={t}"
+        for t in (3, 8):
+            y = h.product(X[:t], exact=True)
+            assert np.array_equal(y.view(np.uint32), one_exact[:t].view(np.uint32)), f"reference order t={t}"
+        worst = 0.0
+        for ks in ("", "1", "3"):
+            if ks:
+                os.environ["Q8_GEMM_KS"] = ks
+            try:
+                for t in (5, 16, 17, 40):
+                    y = h.product(X[:t])
+                    m = assert_parity(y, one[:t], f"t={t} ks={ks or 'planned'} against gemv")
+                    assert_parity(y, f64[:t], f"t={t} ks={ks or 'planned'} against F64")
+                    worst = max(worst, m["max_rel"])
+            finally:
+                os.environ.pop("Q8_GEMM_KS", None)
+        say(f"{rows}x{cols}: largest max-rel between gemm(t)[k] and gemv(x[k]) at t >= 5: {worst:.3e}")
+    finally:
+        h.close()
