@@ -126,6 +126,14 @@ void rt_q8_row(const void *w, long cols, long row, float *z);
 void rt_gemv_dev(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
 /* Y = X W^T, t tokens (1..64), X rows x_stride floats apart (x_stride >= cols, % 4 == 0). */
 void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* rt_gemm_dev that allocates nothing, for callers that cannot call hipMalloc (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). No counterpart in the reference.
+ * The same kernels and the same results, bit for bit; the matrix-core product's K-split partials
+ * (t >= 5) live in a static device array of the library, 32 MiB (8 Mi floats) on every GPU it runs
+ * on, held until the process ends. A product whose partials would exceed it is refused with the
+ * reason. Every call on a GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two runtimes) race. */
+void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* A round of n (1..RT_BATCH) products sharing x, none reading another's y: y[i] = X w[i]^T,
  * w[i] [rows[i] cols], as one launch where the kernel takes the shape (t <= 4), else one after
  * another. The device form of rt_gemv_q x n + rt_gemv_go, which uses the same launch for queued

@@ -46,6 +46,7 @@ _SIGS = {
     "rt_q8_free": (None, [_vp, _vp]),
     "rt_gemv_dev": (None, [_vp, _vp, _long, _long, _vp, _vp]),
     "rt_gemm_dev": (None, [_vp, _vp, _long, _long, _vp, _long, _long, _vp]),
+    "rt_gemm_dev_noalloc": (None, [_vp, _vp, _long, _long, _vp, _long, _long, _vp]),
     "rt_gemv_swiglu_dev": (None, [_vp, _vp, _vp, _long, _long, _vp, _long, _long, _vp]),
     "rt_gemv_round_dev": (None, [_vp, _int, _vp, _vp, _long, _vp, _long, _long, _vp]),
     "rt_dev_alloc": (_vp, [_vp, _long]),

@@ -56,6 +56,12 @@
 
 [[noreturn]] static void fail(const char *fn, const char *why) { failf(fn, "%s", why); }
 
+/* The device scratch of rt_gemm_dev_noalloc: the matrix-core product's K-split partials, at most
+ * Q8_GEMM_PART_MAX floats (32 MiB), in a static array of every GPU the library runs on, so that the
+ * product allocates nothing. Host code never names it: rt_init asks for its address on the device
+ * (hipGetSymbolAddress) and keeps that in the runtime. */
+static __device__ __align__(256) float scratch[Q8_GEMM_PART_MAX];
+
 namespace {
 
 /* a registered weight handle: its shape, and whether the library allocated it (rt_q8_upload and
@@ -98,6 +104,8 @@ struct ctx {
     size_t epi_cap = 0;
     /* the matrix-core product's K-split partials */
     float *part = nullptr;
+    /* the device address of `scratch` on this runtime's GPU (rt_gemm_dev_noalloc's partials) */
+    float *noalloc_part = nullptr;
     /* the greedy next token's candidates */
     void *amax = nullptr;
     size_t amax_cap = 0;
@@ -224,8 +232,10 @@ void reserve_gemm(ctx *c, long rows, long cols, long t)
 }
 
 /* Y = X W^T for t >= 5 tokens, 64 at a time; res != NULL: Y = res + X W^T (res may be Y), added in
- * the matrix-core product's store or partial sum */
-void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, long xs, long t, float *y, const float *res = nullptr)
+ * the matrix-core product's store or partial sum. part != NULL: the K-split partials go there (at
+ * most Q8_GEMM_PART_MAX floats) instead of the runtime's workspace, and nothing is allocated. */
+void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, long xs, long t, float *y, const float *res = nullptr,
+                 float *part = nullptr)
 {
     const q8_stream_t s = (q8_stream_t)c->stream;
     for (long k = 0; k < t; k += 64) {
@@ -240,8 +250,14 @@ void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, lo
             }
             continue;
         }
-        reserve_gemm(c, rows, cols, n);
-        q8_launch_gemm_mfma(s, w, rows, cols, x + k * xs, xs, n, y + k * rows, c->part, res ? res + k * rows : nullptr);
+        if (part) {
+            if (q8_gemm_part_floats(rows, cols, n) > Q8_GEMM_PART_MAX)
+                failf("rt_gemm_dev_noalloc", "the K-split partials of %ld x %ld at %ld tokens exceed the %ld-float scratch", rows, cols, n,
+                      (long)Q8_GEMM_PART_MAX);
+        } else {
+            reserve_gemm(c, rows, cols, n);
+        }
+        q8_launch_gemm_mfma(s, w, rows, cols, x + k * xs, xs, n, y + k * rows, part ? part : c->part, res ? res + k * rows : nullptr);
     }
 }
 
@@ -254,8 +270,9 @@ void launched(const char *what)
     }
 }
 
-/* Y = X W^T (w1 NULL) or SiLU(X W0^T) * (X W1^T), device pointers, on the stream */
-void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y)
+/* Y = X W^T (w1 NULL) or SiLU(X W0^T) * (X W1^T), device pointers, on the stream. part != NULL (a
+ * single product only): the matrix-core product's partials go there, and nothing is allocated. */
+void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y, float *part = nullptr)
 {
     q8_stream_t s = (q8_stream_t)c->stream;
     if (c->ktime_on && c->kt.size() < KT_MAX) {
@@ -279,7 +296,7 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
     if (t <= 4) {
         q8_launch_gemv(s, w0, w1, rows, cols, x, xs, t, y);
     } else if (!w1) {
-        gemm_tokens(c, w0, rows, cols, x, xs, t, y);
+        gemm_tokens(c, w0, rows, cols, x, xs, t, y, nullptr, part);
     } else {
         float *g = reserve_scratch(c, (size_t)(2 * rows * t));
         gemm_tokens(c, w0, rows, cols, x, xs, t, g);
@@ -488,6 +505,15 @@ int rt_init(struct rt *R, int threads)
         return -1;
     }
     __atomic_store_n(c->flag, 0u, __ATOMIC_RELEASE);
+    /* this GPU's copy of the static scratch: its address, asked for once with the device current */
+    if (hipGetSymbolAddress((void **)&c->noalloc_part, HIP_SYMBOL(scratch)) != hipSuccess || !c->noalloc_part) {
+        (void)hipHostFree(c->flag);
+        (void)hipEventDestroy(c->ev0);
+        (void)hipEventDestroy(c->ev1);
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return -1;
+    }
     const char *ex = getenv("Q8_EXACT");
     c->exact = ex && atoi(ex) != 0;
     /* R->team and R->frame belong to the caller, which creates its team before rt_init
@@ -765,6 +791,17 @@ void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float 
     if (t < 1 || x_stride < cols || x_stride % 4)
         fail("rt_gemm_dev", "t >= 1 and x_stride >= cols, a multiple of 4");
     product(c, w, nullptr, rows, cols, x, x_stride, t, y);
+}
+
+void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y)
+{
+    ctx *c = get(R, "rt_gemm_dev_noalloc");
+    check_shape(c, "rt_gemm_dev_noalloc", w, rows, cols);
+    check_dev_ptr("rt_gemm_dev_noalloc", x, "x");
+    check_dev_ptr("rt_gemm_dev_noalloc", y, "y");
+    if (t < 1 || x_stride < cols || x_stride % 4)
+        fail("rt_gemm_dev_noalloc", "t >= 1 and x_stride >= cols, a multiple of 4");
+    product(c, w, nullptr, rows, cols, x, x_stride, t, y, c->noalloc_part);
 }
 
 void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y)
