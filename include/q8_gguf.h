@@ -1,9 +1,9 @@
 /* q8_gguf.h: a GGUF v3 model file's header and tensor table, and the upload of its Q8_0 tensors
  * to HBM for the products of q8_rt.h.
  *
- * The reader follows the reference's header reader (src/host/gguf_reader.h:1-60,
- * gguf_reader.c:166-218): the same fields, the same value text and the same errors, under rt_gguf_
- * names so that both can be linked into one program. The upload follows the reference engine's load
+ * The reader replaces the reference's header reader (src/host/gguf_reader.h:1-60): the same structs
+ * and results (fields, key text, offsets, sizes), under rt_gguf_ names so that both can be linked
+ * into one program; its own error texts. The upload follows the reference engine's load
  * loop (src/card/engine.c:287-316): every Q8_0 tensor once per distinct file offset, so tensors
  * tied by offset share one handle (engine.c:307-310).
  *
@@ -34,10 +34,10 @@ struct rt_gguf_key {
     char name[96];
     uint32_t type;      /* RT_GGUF_* */
     uint32_t elem_type; /* for RT_GGUF_ARR */
-    uint64_t n;         /* array elements, or the full string length */
-    char text[128];     /* the value as text: numbers as printf %u/%d (f32 %.9g, f64 %.17g), bool
-                           true/false; numeric arrays of up to 16 elements in full, space separated,
-                           others empty; strings cut to 127 bytes */
+    uint64_t n;         /* an array's count; a string's length in the file (text may hold less) */
+    char text[128];     /* printable value: integers in decimal, f32 to 9 and f64 to 17 significant
+                           digits, bool true/false, a string's first 127 bytes; an array of at most
+                           16 numbers as its values with one space between, any other array "" */
 };
 
 /* A tensor of the table (gguf_reader.h:25-32), and its HBM handle once uploaded. */
@@ -57,8 +57,8 @@ struct rt_gguf {
     uint32_t version;
     uint64_t file_size;
     uint64_t header_end, data_start;
-    uint64_t data_bytes; /* the sum of all tensors' bytes */
-    uint64_t need;       /* the file size the tensor table requires */
+    uint64_t data_bytes; /* bytes of all tensors together, ties counted each time */
+    uint64_t need;       /* data_start + the end of the furthest tensor: the least size a whole file has */
     uint64_t n_keys, n_tensors;
     struct rt_gguf_key *keys;
     struct rt_gguf_tensor *tensors;
@@ -66,9 +66,12 @@ struct rt_gguf {
     int q8_count;        /* and their number */
 };
 
-/* Reads the header of path into g (gguf_load, gguf_reader.c:166-218). 0, or -1 with "path: reason"
- * in err: the file cannot be opened, its magic is not GGUF, the header ends early, a value type is
- * unknown, a tensor has more than 4 dimensions or an unknown ggml type, or it runs out of memory. */
+/* Reads the header of path into g (in place of gguf_load, gguf_reader.c:166-218). 0, or -1 with
+ * "path: reason" in err, the reason naming the byte where the header went wrong: the file cannot be
+ * opened, does not start with "GGUF", ends inside the header, declares more keys or tensors than
+ * its size could hold, uses a value type GGUF does not define, has a tensor of more than 4
+ * dimensions or of an unknown ggml type, or an alignment of 0. general.alignment is taken from an
+ * integer-typed key (32 when absent). The file is mapped, never read past the header. */
 int rt_gguf_read(struct rt_gguf *g, const char *path, char *err, size_t err_cap);
 /* Frees the tables (gguf_free). Handles are not freed here: rt_gguf_release does that. */
 void rt_gguf_free(struct rt_gguf *g);

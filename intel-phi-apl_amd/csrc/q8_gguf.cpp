@@ -1,14 +1,18 @@
 /* q8_gguf.cpp: the GGUF v3 header reader and the Q8_0 upload of include/q8_gguf.h.
  *
- * A GGUF v3 file is: "GGUF", u32 version, u64 tensor count, u64 key count; the keys (u64-length
- * string name, u32 value type, the value; an array is u32 element type, u64 count, the elements);
- * the tensor table (name, u32 dimension count, u64 dimensions ne0 first, u32 ggml type, u64 offset
- * from the data start); then, at the next multiple of general.alignment (32 by default), the data.
- * Only the header is read here; the upload reads each Q8_0 tensor's bytes with pread.
+ * GGUF v3, little endian: "GGUF", u32 version, u64 tensor count, u64 key count; the keys (a string
+ * name, u32 value type, the value; a string is u64 length + bytes; an array is u32 element type, u64
+ * count, the elements); the tensor table (name, u32 dimension count, u64 dimensions ne0 first, u32
+ * ggml type, u64 offset from the data start); then the data, from the first multiple of
+ * general.alignment (32 when absent) at or after the table's end.
  *
- * The reader's results (fields, value text, errors) are the reference's (src/host/gguf_reader.c:
- * 87-218), checked on synthetic files against it built from its source. One difference: an
- * alignment of 0, on which the reference divides by zero, is an error here. */
+ * The file is mapped read-only and the header parsed in place by a cursor that checks every read
+ * against the bytes left (a count that the rest of the file cannot hold is refused before anything
+ * is allocated for it). Values are decoded to a typed scalar and formatted into the key's text
+ * afterwards. Only the header is touched; the upload reads each Q8_0 tensor's bytes with pread.
+ * Results (fields, key text, offsets, sizes) are held field for field to the reference's reader
+ * (src/host/gguf_reader.c) on synthetic files in the tests; the error texts are this file's own,
+ * with the byte offset where the header went wrong. An alignment of 0 is refused. */
 #include "../../include/q8_gguf.h"
 
 #include <errno.h>
@@ -17,6 +21,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -25,7 +30,7 @@
 namespace {
 
 /* ggml's types: name, elements a block, bytes a block (llama.cpp f5b9bd3 ggml/src/ggml.c
- * type_traits; gguf_reader.c:18-30). Ids without a type (4, 5, 31-33, 36-38) give a null name. */
+ * type_traits). Ids without a type (4, 5, 31-33, 36-38) have no name. */
 struct ggml_type {
     const char *name;
     uint32_t block, bytes;
@@ -73,159 +78,265 @@ ggml_type ggml_type_of(uint32_t id)
     }
 }
 
-/* Bytes of a scalar value type; 0 for a string, an array or an unknown type. */
-size_t scalar_bytes(uint32_t t)
+/* width in bytes of a scalar GGUF value type; 0 for string, array and unknown ids */
+unsigned width_of(uint32_t t)
 {
-    switch (t) {
-    case RT_GGUF_U8: case RT_GGUF_I8: case RT_GGUF_BOOL: return 1;
-    case RT_GGUF_U16: case RT_GGUF_I16: return 2;
-    case RT_GGUF_U32: case RT_GGUF_I32: case RT_GGUF_F32: return 4;
-    case RT_GGUF_U64: case RT_GGUF_I64: case RT_GGUF_F64: return 8;
-    default: return 0;
+    static const unsigned w[] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+    return t < sizeof w / sizeof w[0] ? w[t] : 0;
+}
+
+/* a decoded scalar: its type and its bits, widened */
+struct scalar {
+    uint32_t type;
+    uint64_t bits;
+};
+
+/* the value's text: decimal integers, f32 with 9 and f64 with 17 significant digits (each exact on
+ * a round trip), bool as true/false */
+void format(const scalar &v, char *out, size_t cap)
+{
+    switch (v.type) {
+    case RT_GGUF_U8: case RT_GGUF_U16: case RT_GGUF_U32: case RT_GGUF_U64:
+        snprintf(out, cap, "%" PRIu64, v.bits);
+        break;
+    case RT_GGUF_I8: snprintf(out, cap, "%d", (int)(int8_t)v.bits); break;
+    case RT_GGUF_I16: snprintf(out, cap, "%d", (int)(int16_t)v.bits); break;
+    case RT_GGUF_I32: snprintf(out, cap, "%" PRId32, (int32_t)v.bits); break;
+    case RT_GGUF_I64: snprintf(out, cap, "%" PRId64, (int64_t)v.bits); break;
+    case RT_GGUF_BOOL: snprintf(out, cap, "%s", v.bits ? "true" : "false"); break;
+    case RT_GGUF_F32: {
+        float f;
+        const uint32_t b = (uint32_t)v.bits;
+        memcpy(&f, &b, 4);
+        snprintf(out, cap, "%.9g", (double)f);
+        break;
+    }
+    default: {
+        double d;
+        memcpy(&d, &v.bits, 8);
+        snprintf(out, cap, "%.17g", d);
+        break;
+    }
     }
 }
 
-/* Thrown by the reader; rt_gguf_read turns it into "path: reason". */
-struct bad_file {
-    const char *why;
-};
-
-/* Sequential reads of the header from a stdio stream. */
-class header {
+/* A cursor over the mapped header. Every read checks the bytes left; the first failure is kept
+ * (what, and the offset where it happened) and every later read fails at once. */
+class cursor {
   public:
-    explicit header(FILE *f) : f_(f) {}
+    cursor(const uint8_t *base, uint64_t size) : base_(base), at_(0), size_(size) {}
 
-    [[noreturn]] static void fail(const char *why) { throw bad_file{why}; }
+    bool ok() const { return !what_; }
+    uint64_t offset() const { return at_; }
+    const char *what() const { return what_; }
+    uint64_t where() const { return where_; }
+    uint64_t left() const { return size_ - at_; }
 
-    void read(void *p, size_t n)
+    bool fail(const char *what)
     {
-        if (fread(p, 1, n, f_) != n)
-            fail(feof(f_) ? "unexpected end of file in the header" : strerror(errno));
+        if (!what_) {
+            what_ = what;
+            where_ = at_;
+        }
+        return false;
     }
-    uint32_t u32()
+    /* n bytes at the cursor, or NULL (failed: the header ends inside them) */
+    const uint8_t *take(uint64_t n)
     {
-        uint32_t v;
-        read(&v, 4);
+        if (what_)
+            return nullptr;
+        if (n > left()) {
+            fail("the header ends inside a field");
+            return nullptr;
+        }
+        const uint8_t *p = base_ + at_;
+        at_ += n;
+        return p;
+    }
+    template <class T>
+    T le()
+    {
+        T v = 0;
+        if (const uint8_t *p = take(sizeof(T)))
+            memcpy(&v, p, sizeof(T)); /* GGUF is little endian, as this host */
         return v;
     }
-    uint64_t u64()
+    /* a string: its first cap-1 bytes into buf (NUL-terminated), the full length returned */
+    uint64_t text(char *buf, size_t cap)
     {
-        uint64_t v;
-        read(&v, 8);
-        return v;
-    }
-    void skip(uint64_t n, const char *why)
-    {
-        if (fseeko(f_, (off_t)n, SEEK_CUR) != 0)
-            fail(why);
-    }
-    /* A string (u64 length, bytes): the first cap-1 bytes into buf, the rest skipped; returns the
-     * full length. */
-    uint64_t string(char *buf, size_t cap)
-    {
-        const uint64_t n = u64();
-        const size_t keep = n < cap - 1 ? (size_t)n : cap - 1;
-        read(buf, keep);
+        const uint64_t n = le<uint64_t>();
+        const uint8_t *p = take(n);
+        const size_t keep = p ? (size_t)(n < cap - 1 ? n : cap - 1) : 0;
+        if (keep)
+            memcpy(buf, p, keep);
         buf[keep] = 0;
-        if (n > keep)
-            skip(n - keep, "seek in a string");
         return n;
     }
-    /* One scalar of type t, as text. */
-    void scalar(uint32_t t, char *out, size_t cap)
+    /* one scalar of type t */
+    bool value(uint32_t t, scalar *v)
     {
-        const size_t n = scalar_bytes(t);
-        if (!n)
-            fail("bad value type");
-        unsigned char b[8];
-        read(b, n);
-        union {
-            uint8_t u8;
-            int8_t i8;
-            uint16_t u16;
-            int16_t i16;
-            uint32_t u32;
-            int32_t i32;
-            float f32;
-            uint64_t u64;
-            int64_t i64;
-            double f64;
-        } v;
-        memcpy(&v, b, n);
-        switch (t) {
-        case RT_GGUF_U8: snprintf(out, cap, "%u", (unsigned)v.u8); break;
-        case RT_GGUF_I8: snprintf(out, cap, "%d", (int)v.i8); break;
-        case RT_GGUF_BOOL: snprintf(out, cap, "%s", v.u8 ? "true" : "false"); break;
-        case RT_GGUF_U16: snprintf(out, cap, "%u", (unsigned)v.u16); break;
-        case RT_GGUF_I16: snprintf(out, cap, "%d", (int)v.i16); break;
-        case RT_GGUF_U32: snprintf(out, cap, "%" PRIu32, v.u32); break;
-        case RT_GGUF_I32: snprintf(out, cap, "%" PRId32, v.i32); break;
-        case RT_GGUF_F32: snprintf(out, cap, "%.9g", (double)v.f32); break;
-        case RT_GGUF_U64: snprintf(out, cap, "%" PRIu64, v.u64); break;
-        case RT_GGUF_I64: snprintf(out, cap, "%" PRId64, v.i64); break;
-        default: snprintf(out, cap, "%.17g", v.f64); break;
-        }
+        const unsigned w = width_of(t);
+        if (!w)
+            return fail("a key has a value type GGUF does not define");
+        const uint8_t *p = take(w);
+        if (!p)
+            return false;
+        v->type = t;
+        v->bits = 0;
+        memcpy(&v->bits, p, w);
+        return true;
     }
-    void key(struct rt_gguf_key &k)
-    {
-        string(k.name, sizeof k.name);
-        k.type = u32();
-        k.elem_type = 0;
-        k.n = 1;
-        k.text[0] = 0;
-        if (k.type == RT_GGUF_STR) {
-            k.n = string(k.text, sizeof k.text);
-        } else if (k.type == RT_GGUF_ARR) {
-            k.elem_type = u32();
-            k.n = u64();
-            if (k.elem_type == RT_GGUF_STR) {
-                char none[8];
-                for (uint64_t j = 0; j < k.n; j++)
-                    string(none, sizeof none);
-            } else if (k.n <= 16) {
-                for (uint64_t j = 0; j < k.n; j++) {
-                    char one[32];
-                    scalar(k.elem_type, one, sizeof one);
-                    const size_t at = strlen(k.text);
-                    snprintf(k.text + at, sizeof k.text - at, "%s%s", j ? " " : "", one);
-                }
-            } else {
-                const size_t each = scalar_bytes(k.elem_type);
-                if (!each)
-                    fail("bad value type");
-                skip(k.n * each, "seek over an array");
-            }
-        } else {
-            scalar(k.type, k.text, sizeof k.text);
-        }
-    }
-    void tensor(struct rt_gguf_tensor &t)
-    {
-        string(t.name, sizeof t.name);
-        t.n_dims = u32();
-        if (t.n_dims > 4)
-            fail("tensor with more than 4 dimensions");
-        uint64_t elements = 1;
-        for (uint32_t d = 0; d < t.n_dims; d++)
-            elements *= (t.dim[d] = u64());
-        t.type = u32();
-        t.offset = u64(); /* from the data start; made absolute once it is known */
-        const ggml_type g = ggml_type_of(t.type);
-        if (!g.name)
-            fail("tensor of an unknown ggml type");
-        t.bytes = elements / g.block * g.bytes;
-        t.w = nullptr;
-    }
-    off_t tell() const { return ftello(f_); }
 
   private:
-    FILE *f_;
+    const uint8_t *base_;
+    uint64_t at_, size_;
+    const char *what_ = nullptr;
+    uint64_t where_ = 0;
 };
+
+/* one metadata key into k; its unsigned value in *num when it is an integer scalar */
+bool parse_key(cursor &c, struct rt_gguf_key &k, bool *integer, uint64_t *num)
+{
+    c.text(k.name, sizeof k.name);
+    k.type = c.le<uint32_t>();
+    k.elem_type = 0;
+    k.n = 1;
+    k.text[0] = 0;
+    *integer = false;
+    if (!c.ok())
+        return false;
+    if (k.type == RT_GGUF_STR) {
+        k.n = c.text(k.text, sizeof k.text);
+        return c.ok();
+    }
+    if (k.type != RT_GGUF_ARR) {
+        scalar v;
+        if (!c.value(k.type, &v))
+            return false;
+        format(v, k.text, sizeof k.text);
+        *integer = k.type != RT_GGUF_F32 && k.type != RT_GGUF_F64 && k.type != RT_GGUF_BOOL;
+        *num = v.bits;
+        return true;
+    }
+    k.elem_type = c.le<uint32_t>();
+    k.n = c.le<uint64_t>();
+    if (!c.ok())
+        return false;
+    if (k.elem_type == RT_GGUF_STR) { /* strings: stepped over, no text */
+        for (uint64_t j = 0; j < k.n && c.ok(); j++) {
+            const uint64_t len = c.le<uint64_t>();
+            c.take(len);
+        }
+        return c.ok();
+    }
+    const unsigned w = width_of(k.elem_type);
+    if (!w)
+        return c.fail("an array has an element type GGUF does not define");
+    if (k.n > c.left() / w)
+        return c.fail("the header ends inside an array");
+    if (k.n > 16) { /* long numeric arrays: stepped over, no text */
+        c.take(k.n * w);
+        return c.ok();
+    }
+    size_t at = 0;
+    for (uint64_t j = 0; j < k.n; j++) {
+        scalar v;
+        if (!c.value(k.elem_type, &v))
+            return false;
+        char one[40];
+        format(v, one, sizeof one);
+        at += (size_t)snprintf(k.text + at, at < sizeof k.text ? sizeof k.text - at : 0, j ? " %s" : "%s", one);
+        if (at >= sizeof k.text)
+            at = sizeof k.text - 1;
+    }
+    return true;
+}
+
+/* one entry of the tensor table into t (offset still relative to the data start) */
+bool parse_tensor(cursor &c, struct rt_gguf_tensor &t)
+{
+    c.text(t.name, sizeof t.name);
+    t.n_dims = c.le<uint32_t>();
+    if (!c.ok())
+        return false;
+    if (t.n_dims > 4)
+        return c.fail("a tensor has more than 4 dimensions");
+    uint64_t elements = 1; /* wraps on absurd dimensions: the upload checks those */
+    for (uint32_t d = 0; d < 4; d++) {
+        t.dim[d] = d < t.n_dims ? c.le<uint64_t>() : 0;
+        if (d < t.n_dims)
+            elements *= t.dim[d];
+    }
+    t.type = c.le<uint32_t>();
+    t.offset = c.le<uint64_t>();
+    if (!c.ok())
+        return false;
+    const ggml_type g = ggml_type_of(t.type);
+    if (!g.name)
+        return c.fail("a tensor has a ggml type id this reader does not know");
+    t.bytes = elements / g.block * g.bytes;
+    t.w = nullptr;
+    return true;
+}
 
 void message(char *err, size_t cap, const char *path, const char *why)
 {
     if (err && cap)
         snprintf(err, cap, "%s: %s", path, why);
+}
+
+/* the header of the mapped file into g; false with the reason in why */
+bool parse(struct rt_gguf *g, const uint8_t *base, uint64_t size, char *why, size_t why_cap)
+{
+    cursor c(base, size);
+    const uint8_t *magic = c.take(4);
+    if (magic && memcmp(magic, "GGUF", 4) != 0) {
+        snprintf(why, why_cap, "not a GGUF file: it starts with %02x %02x %02x %02x, not \"GGUF\"", magic[0], magic[1], magic[2], magic[3]);
+        return false;
+    }
+    g->version = c.le<uint32_t>();
+    g->n_tensors = c.le<uint64_t>();
+    g->n_keys = c.le<uint64_t>();
+    /* a key takes at least 12 bytes (empty name, type, a u8), a tensor at least 24 */
+    if (c.ok() && (g->n_keys > c.left() / 12 || g->n_tensors > c.left() / 24))
+        c.fail("the header ends before its keys and tensors (counts larger than the file holds)");
+    if (c.ok()) {
+        g->keys = (struct rt_gguf_key *)calloc(g->n_keys ? g->n_keys : 1, sizeof *g->keys);
+        g->tensors = (struct rt_gguf_tensor *)calloc(g->n_tensors ? g->n_tensors : 1, sizeof *g->tensors);
+        if (!g->keys || !g->tensors) {
+            snprintf(why, why_cap, "out of memory for %" PRIu64 " keys and %" PRIu64 " tensors", g->n_keys, g->n_tensors);
+            return false;
+        }
+    }
+    uint64_t alignment = 32;
+    for (uint64_t i = 0; i < g->n_keys && c.ok(); i++) {
+        bool integer = false;
+        uint64_t num = 0;
+        if (parse_key(c, g->keys[i], &integer, &num) && integer && strcmp(g->keys[i].name, "general.alignment") == 0)
+            alignment = num;
+    }
+    uint64_t data_end = 0;
+    for (uint64_t i = 0; i < g->n_tensors && c.ok(); i++) {
+        struct rt_gguf_tensor &t = g->tensors[i];
+        if (!parse_tensor(c, t))
+            break;
+        g->data_bytes += t.bytes;
+        data_end = t.offset + t.bytes > data_end ? t.offset + t.bytes : data_end;
+    }
+    if (!c.ok()) {
+        snprintf(why, why_cap, "%s (at byte %" PRIu64 " of %" PRIu64 ")", c.what(), c.where(), size);
+        return false;
+    }
+    if (alignment == 0) {
+        snprintf(why, why_cap, "general.alignment is 0");
+        return false;
+    }
+    g->header_end = c.offset();
+    g->data_start = (g->header_end + alignment - 1) / alignment * alignment;
+    g->need = g->data_start + data_end;
+    for (uint64_t i = 0; i < g->n_tensors; i++)
+        g->tensors[i].offset += g->data_start;
+    return true;
 }
 
 } // namespace
@@ -235,55 +346,40 @@ extern "C" {
 int rt_gguf_read(struct rt_gguf *g, const char *path, char *err, size_t err_cap)
 {
     memset(g, 0, sizeof *g);
-    FILE *f = fopen(path, "rb");
+    const int fd = open(path, O_RDONLY);
     struct stat st;
-    if (!f || fstat(fileno(f), &st) != 0) {
+    if (fd < 0 || fstat(fd, &st) != 0) {
         message(err, err_cap, path, strerror(errno));
-        if (f)
-            fclose(f);
+        if (fd >= 0)
+            close(fd);
         return -1;
     }
-    try {
-        header h(f);
-        char magic[4];
-        h.read(magic, 4);
-        if (memcmp(magic, "GGUF", 4) != 0)
-            header::fail("not a GGUF file (magic)");
-        g->version = h.u32();
-        g->n_tensors = h.u64();
-        g->n_keys = h.u64();
-        g->file_size = (uint64_t)st.st_size;
-        g->keys = (struct rt_gguf_key *)calloc(g->n_keys ? g->n_keys : 1, sizeof *g->keys);
-        g->tensors = (struct rt_gguf_tensor *)calloc(g->n_tensors ? g->n_tensors : 1, sizeof *g->tensors);
-        if (!g->keys || !g->tensors)
-            header::fail("out of memory");
-        uint64_t alignment = 32, data_end = 0;
-        for (uint64_t i = 0; i < g->n_keys; i++) {
-            h.key(g->keys[i]);
-            if (strcmp(g->keys[i].name, "general.alignment") == 0)
-                alignment = strtoull(g->keys[i].text, nullptr, 10);
+    if (!S_ISREG(st.st_mode)) {
+        message(err, err_cap, path, S_ISDIR(st.st_mode) ? strerror(EISDIR) : "not a regular file");
+        close(fd);
+        return -1;
+    }
+    g->file_size = (uint64_t)st.st_size;
+    char why[256] = "the header ends inside a field (at byte 0 of 0)";
+    bool ok = false;
+    if (st.st_size > 0) {
+        void *m = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m == MAP_FAILED) {
+            snprintf(why, sizeof why, "%s", strerror(errno));
+        } else {
+            ok = parse(g, (const uint8_t *)m, (uint64_t)st.st_size, why, sizeof why);
+            munmap(m, (size_t)st.st_size);
         }
-        for (uint64_t i = 0; i < g->n_tensors; i++) {
-            struct rt_gguf_tensor &t = g->tensors[i];
-            h.tensor(t);
-            g->data_bytes += t.bytes;
-            if (t.offset + t.bytes > data_end)
-                data_end = t.offset + t.bytes;
-        }
-        if (alignment == 0)
-            header::fail("general.alignment is 0");
-        g->header_end = (uint64_t)h.tell();
-        g->data_start = (g->header_end + alignment - 1) / alignment * alignment;
-        g->need = g->data_start + data_end;
-        for (uint64_t i = 0; i < g->n_tensors; i++)
-            g->tensors[i].offset += g->data_start;
-    } catch (const bad_file &e) {
-        message(err, err_cap, path, e.why);
-        fclose(f);
+    }
+    close(fd);
+    if (!ok) {
+        const uint64_t size = g->file_size;
         rt_gguf_free(g);
+        memset(g, 0, sizeof *g);
+        g->file_size = size;
+        message(err, err_cap, path, why);
         return -1;
     }
-    fclose(f);
     return 0;
 }
 
