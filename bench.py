@@ -145,6 +145,7 @@ def decode_9b(b, steps, warmup):
 
     per_token = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) +
                           alg_bytes(HIDDEN, FFN, 1)) + alg_bytes(VOCAB, HIDDEN, 1)
+    b.layers_9b, b.head_9b = layers, head  # the host-pointer token reuses them
     b.lib.rt_graph_begin(b.R)
     token()
     graph = b.lib.rt_graph_end(b.R)
@@ -341,6 +342,54 @@ def host_pointers(b):
     return out
 
 
+def host_pointer_token(b):
+    """The 9B decode token through the reference's own entry points with host arrays, as its generated
+    code calls them (src/card/rt.h:61-72): per layer rt_gemv (QKV), rt_gemv (out, on QKV's first 4096
+    outputs), rt_gemv_q x 2 + rt_gemv_go (gate and up sharing x, one round), rt_gemv (down, on the
+    gate's outputs: SiLU(g)*u is the caller's host work between the products and is not timed here),
+    each x the previous y in host memory; then rt_gemv (head). The PCIe- and wait-inclusive rate of
+    the same 129 products and 7.23 GB the graph token streams."""
+    layers, head = getattr(b, "layers_9b", None), getattr(b, "head_9b", None)
+    own = layers is None
+    if own:
+        layers = [dict(qkv=b.matrix(QKV, HIDDEN), out=b.matrix(HIDDEN, HIDDEN), gate=b.matrix(FFN, HIDDEN), up=b.matrix(FFN, HIDDEN),
+                       down=b.matrix(HIDDEN, FFN)) for _ in range(LAYERS)]
+        head = b.matrix(VOCAB, HIDDEN)
+    rt = b.rt
+    x0 = np.random.default_rng(4).standard_normal(HIDDEN, dtype=np.float32)
+    yq, yo, yd = np.empty(QKV, np.float32), np.empty(HIDDEN, np.float32), np.empty(HIDDEN, np.float32)
+    g, u, logits = np.empty(FFN, np.float32), np.empty(FFN, np.float32), np.empty(VOCAB, np.float32)
+
+    def token():
+        x = x0
+        for L in layers:
+            rt.gemv(L["qkv"], QKV, HIDDEN, x, yq)
+            rt.gemv(L["out"], HIDDEN, HIDDEN, yq[:HIDDEN], yo)
+            rt.gemv_open()
+            rt.gemv_q(L["gate"], FFN, HIDDEN, yo, g)
+            rt.gemv_q(L["up"], FFN, HIDDEN, yo, u)
+            rt.gemv_go()
+            rt.gemv(L["down"], HIDDEN, FFN, g, yd)
+            x = yd
+        rt.gemv(head, VOCAB, HIDDEN, x, logits)
+
+    token()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        token()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    per = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + 2 * alg_bytes(FFN, HIDDEN, 1) - 4 * HIDDEN +
+                    alg_bytes(HIDDEN, FFN, 1)) + alg_bytes(VOCAB, HIDDEN, 1)
+    if own:
+        for L in layers:
+            for w in L.values():
+                rt.free(w)
+        rt.free(head)
+    return {"ms_per_token": round(ms, 3), "GB/s": round(per / ms / 1e6, 1), "pct_hbm": round(100 * per / ms / 1e6 / HBM_PEAK_GBS, 1),
+            "calls_per_token": 4 * LAYERS + 1, "bytes_per_token": per, "tokens_timed": reps}
+
+
 def epilogues_9b(b):
     """The 9B decode layer with the epilogues around its products (src/apl/qwen35.apl:131-139): QKV
     and the gate+up pair on RMS(x), the output and down products added to the residual stream,
@@ -472,17 +521,18 @@ def cpu_baseline(b, layer, seconds):
     mats = [(rows, cols, host_rows(rows, cols, seed0 + i)) for i, (name, rows, cols) in enumerate(shapes)]
     rng = np.random.default_rng(0)
     nbytes = sum(alg_bytes(r, k, 1) for _, r, k in shapes)
-    try:
+    teams = []
+    flags = "oracle"
+
+    def reference_product(path):
+        """the reference's team product from the build at path (oracle/_ref), its team made here"""
         from oracle_ffi import Reference
 
-        ref = Reference()
-        kind = "reference"
+        ref = Reference(path)
         team = ref.lib.ref_team_create(threads)
         if not team:
             raise OSError("team")
-
-        def prepare(rows, cols, raw):
-            return ref.repack_i(raw, rows, cols)
+        teams.append((ref, team))
 
         def product(form, rows, cols, x, t, y):
             if t == 1:
@@ -490,7 +540,20 @@ def cpu_baseline(b, layer, seconds):
             else:
                 ref.lib.ref_team_gemm_i(c.c_void_p(team), c.c_void_p(form.ctypes.data), rows, cols, c.c_void_p(x.ctypes.data), t,
                                         c.c_void_p(y.ctypes.data))
-        done = lambda: ref.lib.ref_team_destroy(c.c_void_p(team))  # noqa: E731
+        return ref, product
+
+    def done():
+        for ref, team in teams:
+            ref.lib.ref_team_destroy(c.c_void_p(team))
+
+    try:
+        # the value: the reference's code built with its own host flags; beside it, with -mfma
+        ref, product = reference_product(os.path.join(ROOT, "oracle", "_ref", "libref_flags.so"))
+        flags = "-O2 -ffp-contract=off (the reference's host flags, scripts/lib.sh:37)"
+        kind = "reference"
+
+        def prepare(rows, cols, raw):
+            return ref.repack_i(raw, rows, cols)
     except (FileNotFoundError, OSError):
         from oracle_ffi import Oracle
 
@@ -521,10 +584,18 @@ def cpu_baseline(b, layer, seconds):
     try:
         layer_jobs = [job(rows, cols, raw, 1) for rows, cols, raw in mats]
         med, n = median_time(lambda: [product(*j) for j in layer_jobs], seconds)
-        out = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+        out = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind, "flags": flags,
                "sample": f"one 9B decode layer (QKV 6144x4096, out 4096x4096, gate and up 12288x4096, down 4096x12288: {nbytes} B), "
                          f"median of {n} passes after one warm-up, {threads} threads pinned to this host's CPUs",
                "ms_per_layer": round(1e3 * med, 2), "host_cpus": os.cpu_count()}
+        if kind == "reference":
+            try:
+                _, mfma_product = reference_product(os.path.join(ROOT, "oracle", "_ref", "libref.so"))
+                med2, n2 = median_time(lambda: [mfma_product(*j) for j in layer_jobs], seconds / 2)
+                out["variants"] = {"-mfma": {"value": round(nbytes / med2 / 1e9, 3), "unit": "GB/s", "ms_per_layer": round(1e3 * med2, 2),
+                                             "passes": n2, "flags": "-O2 -ffp-contract=off -mfma (fmaf inlined; the same bits)"}}
+            except (FileNotFoundError, OSError):
+                pass
         configs = {}
         # config 1: the 4096x4096 GEMV (seed 0 rows, as the parity fixtures)
         j1 = job(HIDDEN, HIDDEN, host_rows(HIDDEN, HIDDEN, 0), 1)
@@ -723,7 +794,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", metavar="SECTIONS", help="comma-separated sections to run instead of the full line (gemv_4096x4096, "
-                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, gguf_load_9b_layer, epilogues_9b); prints their results only")
+                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, host_pointer_token_9b, gguf_load_9b_layer, "
+                    "epilogues_9b); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
     ap.add_argument("--summarize-gemm", metavar="DIR", help="write the GEMM rocprofv3 summary under profiles/ from DIR and exit")
@@ -746,6 +818,7 @@ def main():
     log(f"device: {name}, {cus} CUs")
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
                 ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers),
+                ("host_pointer_token_9b", host_pointer_token),
                 ("gguf_load_9b_layer", gguf_load), ("epilogues_9b", epilogues_9b))
     if a.only:
         want = a.only.split(",")

@@ -77,8 +77,9 @@ void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, 
  * (rt.h:63-69; rt.c:251-265, 274-285) */
 #define RT_BATCH 8
 void rt_gemv_q(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
-/* Opens the round before x is ready (rt.c:267-272). Nothing to read ahead on the GPU: the
- * weights are already in HBM. Kept so generated code links; it does nothing. */
+/* Opens the round before x is ready (rt.c:267-272). Reads nothing ahead: on the MI355X a read of the
+ * queued weights into the Infinity Cache while x is prepared makes the round slower, not faster
+ * (the products read the bytes again). Kept so generated code links; it does nothing. */
 void rt_gemv_open(struct rt *R);
 void rt_gemv_go(struct rt *R);
 

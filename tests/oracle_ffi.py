@@ -140,10 +140,11 @@ class Oracle:
 class Reference:
     """The reference's own gemv.c / gemm.c / team.c, compiled from its sources into oracle/_ref."""
 
-    def __init__(self):
-        if not os.path.exists(REF_SO):
-            raise FileNotFoundError(REF_SO)
-        self.lib = c.CDLL(REF_SO)
+    def __init__(self, path=None):
+        path = path or REF_SO
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = c.CDLL(path)
         L = self.lib
         L.ref_gemv.argtypes = [_vp, _l, _l, _vp, _vp]
         L.ref_gemm.argtypes = [_vp, _l, _l, _vp, _l, _vp]

@@ -324,3 +324,19 @@ def test_swiglu_f64_pinned(oracle):
     with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         for name, f in planted.items():
             assert swiglu_violations(f), f"the planted mistake '{name}' passes every check"
+
+
+def test_reference_flag_builds_agree():
+    """The reference's host model built with its own flags (-O2 -ffp-contract=off, fmaf a libm call)
+    and with -mfma (fmaf inlined) give the same bits: fmaf is correctly rounded either way. Both are
+    timed as the CPU baseline."""
+    from oracle_ffi import ORACLE_DIR, Reference
+
+    paths = [os.path.join(ORACLE_DIR, "_ref", n) for n in ("libref.so", "libref_flags.so")]
+    if not all(os.path.exists(p) for p in paths):
+        pytest.skip("oracle/_ref is not built")
+    a, b = Reference(paths[0]), Reference(paths[1])
+    for seed, rows, cols, t in [(61, 64, 512, 1), (62, 48, 1024, 5), (63, 128, 256, 17)]:
+        q8, x = synth.case(seed, rows, cols, t, "lognormal" if seed % 2 else "normal")
+        ya, yb = a.gemm(q8, rows, cols, x), b.gemm(q8, rows, cols, x)
+        assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (rows, cols, t)
