@@ -255,7 +255,10 @@ def verify_path(b):
         for (kind, rows, cols, t), v in kt.items():
             pair = kind.endswith("pair")
             us = statistics.fmean(v)
-            res["fused_gate_up" if pair else "down"] = {"kernel_us": round(us, 3), "GB/s": round(alg_bytes(rows, cols, t, pair) / us / 1e3, 1)}
+            kname, grid = b.knames[(kind, rows, cols, t)]
+            res["fused_gate_up" if pair else "down"] = {"kernel_us": round(us, 3), "GB/s": round(alg_bytes(rows, cols, t, pair) / us / 1e3, 1),
+                                                          "pct_hbm": round(100 * alg_bytes(rows, cols, t, pair) / us / 1e3 / HBM_PEAK_GBS, 1),
+                                                          "kernel": kname, "grid": grid}
         out[f"M{m}"] = res
     for s in sets:
         for w in s:
@@ -764,6 +767,70 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
     print(f"wrote {out}")
 
 
+VERIFY_PROFILE = os.path.join(PROFILES, "gemv_verify_9b_m2_m4.md")
+VERIFY_PROFILE_CMDS = [
+    "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/vprof_stats -o run -- python3 bench.py --only verify "
+    "> gpurun_out/vprof_stats.log 2>&1",
+    "rocprofv3 --pmc FETCH_SIZE GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/vprof_fetch -o run -- python3 bench.py --only verify",
+    "rocprofv3 --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VMEM "
+    "SQ_INSTS_VMEM_RD GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/vprof_sq -o run -- python3 bench.py --only verify",
+    "python3 bench.py --summarize-verify gpurun_out",
+]
+
+
+def summarize_verify(run_dir, out=VERIFY_PROFILE, xcds=8, simds=1024):
+    """profiles/gemv_verify_9b_m2_m4.md from the three rocprofv3 runs of VERIFY_PROFILE_CMDS: per verify
+    kernel (the fused gate+up pair and down at M = 2, 3, 4), its mean duration (kernel trace), HBM
+    bytes (FETCH_SIZE x2, as for the decode profile), VALU instructions a weight, the share of the
+    SIMDs' cycles spent issuing VALU (SQ_INSTS_VALU x 4 cycles of a wave64 instruction over
+    GRBM_GUI_ACTIVE / XCDs x SIMDs), the waves resident a SIMD (SQ_WAVE_CYCLES, in quad-cycles, x 4
+    over the same) and the
+    share of the waves' cycles spent waiting (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES)."""
+    import csv
+    from collections import defaultdict
+
+    line = json.loads(next(l for l in open(os.path.join(run_dir, "vprof_stats.log")) if l.startswith('{"verify"')))["verify"]
+    trace = defaultdict(list)
+    for r in csv.DictReader(open(os.path.join(run_dir, "vprof_stats", "run_kernel_trace.csv"))):
+        g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        trace[(_kname(r["Kernel_Name"]), g)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    cnt = defaultdict(lambda: defaultdict(list))
+    for sub in ("vprof_fetch", "vprof_sq"):
+        for r in csv.DictReader(open(os.path.join(run_dir, sub, "run_counter_collection.csv"))):
+            cnt[(_kname(r["Kernel_Name"]), int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    mean = lambda v: statistics.fmean(v) if v else float("nan")  # noqa: E731
+    rows = []
+    for m, res in line.items():
+        t = int(m[1:])
+        for what, k in res.items():
+            pair = what == "fused_gate_up"
+            r_, c_ = (FFN, HIDDEN) if pair else (HIDDEN, FFN)
+            key = (k["kernel"], k["grid"])
+            c = cnt.get(key, {})
+            gui = mean(c.get("GRBM_GUI_ACTIVE", []))
+            simd_cycles = gui / xcds * simds
+            weights = (2 if pair else 1) * r_ * c_
+            valu = mean(c.get("SQ_INSTS_VALU", []))
+            rows.append(f"| M={t} | {'gate+up pair' if pair else 'down'} {r_}x{c_} | `{k['kernel']}` | {mean(trace.get(key, [])):.2f} | {k['kernel_us']:.2f} | "
+                        f"{100 * alg_bytes(r_, c_, t, pair) / k['kernel_us'] / 1e3 / HBM_PEAK_GBS:.1f} | {2.0 * mean(c.get('FETCH_SIZE', [])) * 1024 / 1e6:.1f} | "
+                        f"{alg_bytes(r_, c_, t, pair) / 1e6:.1f} | {64 * valu / weights:.2f} | {100 * 4 * valu / simd_cycles:.1f} | "
+                        f"{4 * mean(c.get('SQ_WAVE_CYCLES', [])) / simd_cycles:.2f} | {100 * mean(c.get('SQ_WAIT_INST_ANY', [])) / mean(c.get('SQ_WAVE_CYCLES', [])):.1f} |")
+    text = ["# Speculative-verify products at 9B shapes, M = 2..4 tokens (rocprofv3)", "",
+            "Workload: the fused gate+up pair SiLU(X Wg^T) * (X Wu^T), 2 x 12288x4096, then down 4096x12288, X F32 [M x cols], "
+            "scales d = binary16(lognormal(ln 0.002, 1)), each product over >= 512 MB of rotated weight copies.", "",
+            "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + VERIFY_PROFILE_CMDS + ["```", "",
+            "| M | Product | Kernel | Trace avg us | Bench kernel us | % of HBM peak | HBM MB (FETCH_SIZE x2) | Algorithmic MB | "
+            "VALU instructions a weight (x64 lanes) | VALU issue % of SIMD cycles | Waves a SIMD | Wave cycles waiting % |",
+            "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    text += rows
+    text += ["", f"VALU instructions a weight = SQ_INSTS_VALU x 64 lanes / weights (the pair counts both matrices). VALU issue % = "
+             f"SQ_INSTS_VALU x 4 cycles (a wave64 instruction on a 16-lane SIMD) / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). "
+             "Waves a SIMD = SQ_WAVE_CYCLES (counted in quad-cycles, so x 4) over the same SIMD cycles; wave cycles waiting = "
+             "SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (both in quad-cycles). Counters are per (kernel, grid).", ""]
+    open(out, "w").write("\n".join(text))
+    print(f"wrote {out}")
+
+
 def profiled_traffic(kname, grid, path=DECODE_PROFILE):
     """HBM bytes per launch of (kernel, grid) from the committed rocprofv3 summary, or None."""
     try:
@@ -799,6 +866,7 @@ def main():
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
     ap.add_argument("--summarize-gemm", metavar="DIR", help="write the GEMM rocprofv3 summary under profiles/ from DIR and exit")
+    ap.add_argument("--summarize-verify", metavar="DIR", help="write the verify-path rocprofv3 summary under profiles/ from DIR and exit")
     ap.add_argument("--calib", action="store_true", help="also copy 1 GiB three times with the plain copy kernel (the yardstick "
                     "for the HBM byte counters of a rocprofv3 --pmc run)")
     a = ap.parse_args()
@@ -807,6 +875,9 @@ def main():
         return
     if a.summarize_gemm:
         summarize_gemm(a.summarize_gemm)
+        return
+    if a.summarize_verify:
+        summarize_verify(a.summarize_verify)
         return
     if a.gpus != 1:
         print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (every product runs on one MI355X; see DESIGN.md "

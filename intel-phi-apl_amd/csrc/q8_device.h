@@ -116,6 +116,13 @@ extern long *q8_next_grid;
 
 /* Y = X W^T, t tokens, the fast kernels; W form S. w1 != NULL: the fused pair, Y = SiLU(X W0^T) * (X W1^T). */
 void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
+/* The same for t = 3 and 4 on the matrix cores (q8_mx.hip), res != NULL: Y = res + the product
+ * (not with the pair; res may be y): true when launched, false when the kernel does not take the
+ * shape (nothing launched). q8_gemv_mx_takes says which: the decode product, its fused residual
+ * and the round all route on it, so that a product's bits do not depend on the entry point. */
+bool q8_launch_gemv_mx(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y,
+                       const float *res = nullptr);
+bool q8_gemv_mx_takes(long rows, long cols, long t);
 /* An epilogue on either side of a product (src/apl/qwen35.apl:49, 131-139). nw != NULL: the RMS
  * norm first, per token xn[k] = nw[k] * (x[k] * s) with s = 1 / sqrt(eps + sum_k x[k]^2 / cols);
  * res != NULL: Y = res + the product, res laid out as Y (it may be Y: the residual stream updated

@@ -403,6 +403,8 @@ static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, lo
 {
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
     const long kb = cols % 1024 ? 0 : cols / 1024;
+    if (MT >= 3 && q8_launch_gemv_mx(s, a, b, rows, cols, x, xs, MT, y))
+        return;
     int rw, nw;
     gemv_choose(PAIR, MT, rows, kb, &rw, &nw);
     if (kb && rows % rw == 0) {
@@ -499,6 +501,10 @@ int q8_launch_gemv_epi(q8_stream_t stream, const void *w0, const void *w1, long 
 {
     if (t < 1 || t > 4 || (e.nw != nullptr) == (e.res != nullptr) || (w1 && e.res))
         return -1;
+    /* the residual of a product the matrix-core decode kernel takes: added in its store, so that
+     * the bits are that product's plus one F32 add */
+    if (e.res && q8_gemv_mx_takes(rows, cols, t))
+        return q8_launch_gemv_mx(stream, w0, w1, rows, cols, x, x_stride, t, y, e.res) ? 0 : -1;
     hipStream_t s = (hipStream_t)stream;
     bool done;
     switch (t) {
@@ -635,6 +641,11 @@ int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const 
     long kb;
     if (!round_plan(n, w, rows, cols, t, y, r, nw, kb))
         return -1;
+    /* a product the matrix-core decode kernel takes runs as its own launch, so that its bits are
+     * the single product's */
+    for (int i = 0; i < n; i++)
+        if (q8_gemv_mx_takes(rows[i], cols, t))
+            return -1;
     constexpr int RW = ROUND_RW;
     hipStream_t s = (hipStream_t)stream;
     bool done = false;

@@ -231,6 +231,20 @@ void reserve_gemm(ctx *c, long rows, long cols, long t)
         fail("the matrix-core product", "its K-split partials exceed the workspace (a planning error)");
 }
 
+/* Whether t tokens of a product go to the matrix-core product (else the decode kernels, which take
+ * at most 4): from 5 tokens on. Q8_MFMA_MIN_T = n (1..5) moves the threshold down, for measuring
+ * the two on the same shapes (the matrix-core decode kernel at 3 and 4 tokens is faster than the
+ * product at the 9B shapes, so the threshold stays). */
+bool on_matrix_cores(long t)
+{
+    static long min_t = -1;
+    if (min_t < 0) {
+        const char *v = getenv("Q8_MFMA_MIN_T");
+        min_t = v && atol(v) >= 1 && atol(v) <= 5 ? atol(v) : 5;
+    }
+    return t >= min_t;
+}
+
 /* Y = X W^T for t >= 5 tokens, 64 at a time; res != NULL: Y = res + X W^T (res may be Y), added in
  * the matrix-core product's store or partial sum. part != NULL: the K-split partials go there (at
  * most Q8_GEMM_PART_MAX floats) instead of the runtime's workspace, and nothing is allocated. */
@@ -240,7 +254,7 @@ void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, lo
     const q8_stream_t s = (q8_stream_t)c->stream;
     for (long k = 0; k < t; k += 64) {
         const long n = t - k < 64 ? t - k : 64;
-        if (n <= 4) {
+        if (!on_matrix_cores(n)) {
             if (!res) {
                 q8_launch_gemv(s, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows);
             } else if (q8_launch_gemv_epi(s, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows, q8_epi{nullptr, 0.0f, res + k * rows}) != 0) {
@@ -277,7 +291,7 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
     q8_stream_t s = (q8_stream_t)c->stream;
     if (c->ktime_on && c->kt.size() < KT_MAX) {
         const size_t i = c->kt.size();
-        const int kind = c->exact ? RT_K_EXACT : (t <= 4 ? RT_K_GEMV : RT_K_GEMM) + (w1 ? 1 : 0);
+        const int kind = c->exact ? RT_K_EXACT : (on_matrix_cores(t) ? RT_K_GEMM : RT_K_GEMV) + (w1 ? 1 : 0);
         c->kt.push_back(ktrec{kind, rows, cols, t, 0, {0}});
         q8_time_next(c->kt_events[2 * i], c->kt_events[2 * i + 1], c->kt.back().name, &c->kt.back().grid);
     }
@@ -293,7 +307,7 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
         launched("the reference-order product");
         return;
     }
-    if (t <= 4) {
+    if (!on_matrix_cores(t)) {
         q8_launch_gemv(s, w0, w1, rows, cols, x, xs, t, y);
     } else if (!w1) {
         gemm_tokens(c, w0, rows, cols, x, xs, t, y, nullptr, part);
