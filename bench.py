@@ -772,8 +772,8 @@ VERIFY_PROFILE_CMDS = [
     "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/vprof_stats -o run -- python3 bench.py --only verify "
     "> gpurun_out/vprof_stats.log 2>&1",
     "rocprofv3 --pmc FETCH_SIZE GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/vprof_fetch -o run -- python3 bench.py --only verify",
-    "rocprofv3 --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VMEM "
-    "SQ_INSTS_VMEM_RD GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/vprof_sq -o run -- python3 bench.py --only verify",
+    "rocprofv3 --pmc SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_WAIT_INST_ANY SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES "
+    "SQ_INSTS_VMEM_RD SQ_INSTS_LDS GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/vprof_sq -o run -- python3 bench.py --only verify",
     "python3 bench.py --summarize-verify gpurun_out",
 ]
 
@@ -781,11 +781,12 @@ VERIFY_PROFILE_CMDS = [
 def summarize_verify(run_dir, out=VERIFY_PROFILE, xcds=8, simds=1024):
     """profiles/gemv_verify_9b_m2_m4.md from the three rocprofv3 runs of VERIFY_PROFILE_CMDS: per verify
     kernel (the fused gate+up pair and down at M = 2, 3, 4), its mean duration (kernel trace), HBM
-    bytes (FETCH_SIZE x2, as for the decode profile), VALU instructions a weight, the share of the
-    SIMDs' cycles spent issuing VALU (SQ_INSTS_VALU x 4 cycles of a wave64 instruction over
-    GRBM_GUI_ACTIVE / XCDs x SIMDs), the waves resident a SIMD (SQ_WAVE_CYCLES, in quad-cycles, x 4
-    over the same) and the
-    share of the waves' cycles spent waiting (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES)."""
+    bytes (FETCH_SIZE x2, as for the decode profile), VALU instructions a weight (MFMA ones
+    included), the share of the SIMDs' cycles spent issuing VALU (SQ_INSTS_VALU x 4 cycles of a
+    wave64 instruction over GRBM_GUI_ACTIVE / XCDs x SIMDs), MFMA instructions a weight and the
+    share of the SIMDs' cycles their matrix cores are busy (SQ_VALU_MFMA_BUSY_CYCLES over the same),
+    the waves resident a SIMD (SQ_WAVE_CYCLES, in quad-cycles, x 4 over the same) and the share of
+    the waves' cycles spent waiting (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES)."""
     import csv
     from collections import defaultdict
 
@@ -811,19 +812,24 @@ def summarize_verify(run_dir, out=VERIFY_PROFILE, xcds=8, simds=1024):
             simd_cycles = gui / xcds * simds
             weights = (2 if pair else 1) * r_ * c_
             valu = mean(c.get("SQ_INSTS_VALU", []))
+            mfma = mean(c.get("SQ_INSTS_MFMA", []))
             rows.append(f"| M={t} | {'gate+up pair' if pair else 'down'} {r_}x{c_} | `{k['kernel']}` | {mean(trace.get(key, [])):.2f} | {k['kernel_us']:.2f} | "
                         f"{100 * alg_bytes(r_, c_, t, pair) / k['kernel_us'] / 1e3 / HBM_PEAK_GBS:.1f} | {2.0 * mean(c.get('FETCH_SIZE', [])) * 1024 / 1e6:.1f} | "
                         f"{alg_bytes(r_, c_, t, pair) / 1e6:.1f} | {64 * valu / weights:.2f} | {100 * 4 * valu / simd_cycles:.1f} | "
+                        f"{64 * mfma / weights:.3f} | {100 * mean(c.get('SQ_VALU_MFMA_BUSY_CYCLES', [])) / simd_cycles:.1f} | "
                         f"{4 * mean(c.get('SQ_WAVE_CYCLES', [])) / simd_cycles:.2f} | {100 * mean(c.get('SQ_WAIT_INST_ANY', [])) / mean(c.get('SQ_WAVE_CYCLES', [])):.1f} |")
     text = ["# Speculative-verify products at 9B shapes, M = 2..4 tokens (rocprofv3)", "",
             "Workload: the fused gate+up pair SiLU(X Wg^T) * (X Wu^T), 2 x 12288x4096, then down 4096x12288, X F32 [M x cols], "
             "scales d = binary16(lognormal(ln 0.002, 1)), each product over >= 512 MB of rotated weight copies.", "",
             "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + VERIFY_PROFILE_CMDS + ["```", "",
             "| M | Product | Kernel | Trace avg us | Bench kernel us | % of HBM peak | HBM MB (FETCH_SIZE x2) | Algorithmic MB | "
-            "VALU instructions a weight (x64 lanes) | VALU issue % of SIMD cycles | Waves a SIMD | Wave cycles waiting % |",
-            "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+            "VALU instructions a weight (x64 lanes) | VALU issue % of SIMD cycles | MFMA instructions a weight (x64) | MFMA busy % of SIMD cycles | "
+            "Waves a SIMD | Wave cycles waiting % |",
+            "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
     text += rows
-    text += ["", f"VALU instructions a weight = SQ_INSTS_VALU x 64 lanes / weights (the pair counts both matrices). VALU issue % = "
+    text += ["", f"VALU instructions a weight = SQ_INSTS_VALU x 64 lanes / weights (the pair counts both matrices; MFMA instructions are "
+             "counted in it too). MFMA instructions a weight = SQ_INSTS_MFMA x 64 / weights (v_mfma_f32_4x4x1_16b_f32 takes 64 weights, 1.0); "
+             "MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES over the SIMD cycles below. VALU issue % = "
              f"SQ_INSTS_VALU x 4 cycles (a wave64 instruction on a 16-lane SIMD) / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). "
              "Waves a SIMD = SQ_WAVE_CYCLES (counted in quad-cycles, so x 4) over the same SIMD cycles; wave cycles waiting = "
              "SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (both in quad-cycles). Counters are per (kernel, grid).", ""]

@@ -72,6 +72,45 @@ __device__ __forceinline__ float q8_wave_sum_dpp(float v)
     return (r0 + r1) + (r2 + r3);
 }
 
+/* v[c] of lane j of each quad (lanes 4b..4b+3) <- v[j] of lane c: a 4x4 transpose inside the quad,
+ * in two exchanges (lanes j^1, then j^2). Each step is one v_cndmask_b32 whose first operand is
+ * read through DPP from the partner lane: out = vcc ? keep : partner's value, with vcc the lanes
+ * that keep (lanes whose bit 0, then bit 1, equals that of c). */
+#define Q8_QT_STEP(out, keep, give, perm, mask)                                                                        \
+    asm volatile("s_mov_b32 vcc_lo, " mask "\n\ts_mov_b32 vcc_hi, " mask "\n\tv_cndmask_b32_dpp %0, %1, %2, vcc " perm   \
+                 " row_mask:0xf bank_mask:0xf"                                                                         \
+                 : "=v"(out)                                                                                           \
+                 : "v"(give), "v"(keep)                                                                                \
+                 : "vcc")
+__device__ __forceinline__ void q8_quad_transpose(uint32_t (&v)[4], int j)
+{
+    (void)j;
+    uint32_t a[4];
+    /* c even keeps in lanes with j even (0x5555...), c odd in lanes with j odd (0xaaaa...) */
+    Q8_QT_STEP(a[0], v[0], v[1], "quad_perm:[1,0,3,2]", "0x55555555");
+    Q8_QT_STEP(a[2], v[2], v[3], "quad_perm:[1,0,3,2]", "0x55555555");
+    Q8_QT_STEP(a[1], v[1], v[0], "quad_perm:[1,0,3,2]", "0xaaaaaaaa");
+    Q8_QT_STEP(a[3], v[3], v[2], "quad_perm:[1,0,3,2]", "0xaaaaaaaa");
+    /* c < 2 keeps in lanes with j < 2 (0x3333...), c >= 2 in lanes with j >= 2 (0xcccc...) */
+    Q8_QT_STEP(v[0], a[0], a[2], "quad_perm:[2,3,0,1]", "0x33333333");
+    Q8_QT_STEP(v[1], a[1], a[3], "quad_perm:[2,3,0,1]", "0x33333333");
+    Q8_QT_STEP(v[2], a[2], a[0], "quad_perm:[2,3,0,1]", "0xcccccccc");
+    Q8_QT_STEP(v[3], a[3], a[1], "quad_perm:[2,3,0,1]", "0xcccccccc");
+}
+#undef Q8_QT_STEP
+
+/* the same for four 16-byte registers, component by component */
+__device__ __forceinline__ void q8_quad_transpose4(uint4 (&v)[4], int j)
+{
+    uint32_t t[4];
+#define Q8_QT(f)                                                                                                       \
+    t[0] = v[0].f, t[1] = v[1].f, t[2] = v[2].f, t[3] = v[3].f;                                                        \
+    q8_quad_transpose(t, j);                                                                                           \
+    v[0].f = t[0], v[1].f = t[1], v[2].f = t[2], v[3].f = t[3];
+    Q8_QT(x) Q8_QT(y) Q8_QT(z) Q8_QT(w)
+#undef Q8_QT
+}
+
 /* SiLU(g) * u (src/apl/qwen35.apl:38; docs/model.md:29: Sig = 1 / (1 + exp(min(700, -g)))):
  * in binary32 exp(min(700, -g)) overflows to inf for -g > 88.7 exactly as exp(-g) does, so
  * the clamp changes nothing and is left out. */
