@@ -51,14 +51,24 @@ void ref_gemm(const uint8_t *q8, long rows, long cols, const float *x, long t, f
     free(w);
 }
 
+/* The CPUs this thread may use before the first team: the team pins its calling thread to its
+ * first CPU, so later teams read the set from here, and ref_team_destroy gives the thread the
+ * whole set back (a second team, in the same process, sees the same CPUs as the first). */
+static cpu_set_t first_allowed;
+static int have_allowed;
+
 void *ref_team_create(int n)
 {
     cpu_set_t allowed;
     int *cpus = malloc(sizeof(int) * (size_t)n), k = 0;
     if (!cpus)
         abort();
-    CPU_ZERO(&allowed);
-    sched_getaffinity(0, sizeof allowed, &allowed);
+    if (!have_allowed) {
+        CPU_ZERO(&first_allowed);
+        sched_getaffinity(0, sizeof first_allowed, &first_allowed);
+        have_allowed = 1;
+    }
+    allowed = first_allowed;
     for (int c = 0; c < CPU_SETSIZE && k < n; c++)
         if (CPU_ISSET((size_t)c, &allowed))
             cpus[k++] = c;
@@ -71,7 +81,12 @@ void *ref_team_create(int n)
     return t;
 }
 
-void ref_team_destroy(void *t) { team_destroy(t); }
+void ref_team_destroy(void *t)
+{
+    team_destroy(t);
+    if (have_allowed)
+        sched_setaffinity(0, sizeof first_allowed, &first_allowed);
+}
 
 void ref_team_gemv_i(void *team, const void *form_i, long rows, long cols, const float *x, float *y)
 {

@@ -1,7 +1,8 @@
-"""The benchmark's profile writers (bench.summarize, bench.summarize_gemm) on small synthetic runs in
-rocprofv3's CSV layout: each product is matched to its own kernel and grid (two products that share
-a kernel name on different grids stay apart), trace averages and counter scaling come out as
-computed by hand, and the matrix-core table counts the x-resident kernel as one token tile."""
+"""The benchmark's profile writers (bench.summarize, bench.summarize_gemm, bench.summarize_verify) on
+small synthetic runs in rocprofv3's CSV layout: each product is matched to its own kernel and grid
+(two products that share a kernel name on different grids stay apart), trace averages and counter
+scaling come out as computed by hand, and the matrix-core table counts the x-resident kernel as one
+token tile."""
 import csv
 import json
 import os
@@ -91,3 +92,36 @@ def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path):
     for s in shapes:
         assert rows[s][-1] == "1.000", s  # counted / issued: one token tile for gemm_xres, three for gemm_mfma<3, ...>
         assert rows[s][-2] == "10.0", s   # MFMA busy: 1024 cycles over (80 / 8 XCDs x 1024 SIMDs)
+
+
+def test_verify_summary_per_kernel_and_grid(tmp_path):
+    """bench.summarize_verify: each verify product (M, pair or down) is matched to its own kernel and
+    grid; counters per weight and per SIMD cycle as computed by hand (GRBM_GUI_ACTIVE summed over 8
+    XCDs, 1024 SIMDs, SQ_WAVE_CYCLES and SQ_WAIT_INST_ANY in quad-cycles)."""
+    run = tmp_path / "run"
+    F, H = bench.FFN, bench.HIDDEN
+    pk, dk = "gemv_mx<4, 4, 1, 4, 1, 0>", "gemv_mx<4, 12, 0, 4, 2, 0>"
+    line = {"verify": {"M4": {"fused_gate_up": {"kernel_us": 30.0, "kernel": pk, "grid": 196608},
+                              "down": {"kernel_us": 20.0, "kernel": dk, "grid": 196608}}}}
+    os.makedirs(run)
+    (run / "vprof_stats.log").write_text("noise\n" + json.dumps(line) + "\n")
+    _trace(str(run / "vprof_stats" / "run_kernel_trace.csv"), [(pk, 196608, [28.0, 28.4]), (dk, 196608, [16.5])])
+    _counters(str(run / "vprof_fetch" / "run_counter_collection.csv"), [(pk, 196608, "FETCH_SIZE", [50000.0]), (dk, 196608, "FETCH_SIZE", [25000.0])])
+    gui = 8.0 * 1000  # 1000 cycles a XCD: 1024000 SIMD cycles
+    vals = []
+    for k, w in ((pk, 2 * F * H), (dk, H * F)):
+        vals += [(k, 196608, "SQ_INSTS_VALU", [w / 64 * 4.0]), (k, 196608, "SQ_INSTS_MFMA", [w / 64]), (k, 196608, "GRBM_GUI_ACTIVE", [gui]),
+                 (k, 196608, "SQ_VALU_MFMA_BUSY_CYCLES", [102400.0]), (k, 196608, "SQ_WAVE_CYCLES", [512000.0]),
+                 (k, 196608, "SQ_WAIT_INST_ANY", [128000.0])]
+    _counters(str(run / "vprof_sq" / "run_counter_collection.csv"), vals)
+    out = tmp_path / "verify.md"
+    bench.summarize_verify(str(run), out=str(out))
+    rows = [[c.strip() for c in l.split("|")[1:-1]] for l in out.read_text().splitlines() if l.startswith("| M=")]
+    assert [r[1].split()[0] for r in rows] == ["gate+up", "down"]
+    pair, down = rows
+    assert pair[2] == f"`{pk}`" and pair[3] == "28.20" and down[3] == "16.50"
+    assert pair[6] == f"{2.0 * 50000 * 1024 / 1e6:.1f}" and down[6] == f"{2.0 * 25000 * 1024 / 1e6:.1f}"  # FETCH_SIZE x2, KiB
+    for r in rows:
+        assert r[8] == "4.00" and r[10] == "1.000"  # VALU and MFMA instructions a weight
+        assert r[11] == "10.0"                      # MFMA busy: 102400 / 1024000
+        assert r[12] == "2.00" and r[13] == "25.0"  # waves a SIMD: 4 x 512000 / 1024000; waiting 128000 / 512000
