@@ -161,7 +161,7 @@ void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long row
  * and the round all route on it, so that a product's bits do not depend on the entry point. */
 bool q8_launch_gemv_mx(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y,
                        const float *res = nullptr);
-bool q8_gemv_mx_takes(long rows, long cols, long t);
+bool q8_gemv_mx_takes(long rows, long cols, long t, bool pair);
 /* An epilogue on either side of a product (src/apl/qwen35.apl:49, 131-139). nw != NULL: the RMS
  * norm first, per token xn[k] = nw[k] * (x[k] * s) with s = 1 / sqrt(eps + sum_k x[k]^2 / cols);
  * res != NULL: Y = res + the product, res laid out as Y (it may be Y: the residual stream updated

@@ -503,7 +503,7 @@ int q8_launch_gemv_epi(q8_stream_t stream, const void *w0, const void *w1, long 
         return -1;
     /* the residual of a product the matrix-core decode kernel takes: added in its store, so that
      * the bits are that product's plus one F32 add */
-    if (e.res && q8_gemv_mx_takes(rows, cols, t))
+    if (e.res && q8_gemv_mx_takes(rows, cols, t, false))
         return q8_launch_gemv_mx(stream, w0, w1, rows, cols, x, x_stride, t, y, e.res) ? 0 : -1;
     hipStream_t s = (hipStream_t)stream;
     bool done;
@@ -644,7 +644,7 @@ int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const 
     /* a product the matrix-core decode kernel takes runs as its own launch, so that its bits are
      * the single product's */
     for (int i = 0; i < n; i++)
-        if (q8_gemv_mx_takes(rows[i], cols, t))
+        if (q8_gemv_mx_takes(rows[i], cols, t, false))
             return -1;
     constexpr int RW = ROUND_RW;
     hipStream_t s = (hipStream_t)stream;

@@ -177,9 +177,22 @@ static int mx_choose(long rows, long cols)
     return 1;
 }
 
-bool q8_gemv_mx_takes(long rows, long cols, long t)
+/* Whether the kernel takes t tokens of a product: a shape it runs (mx_choose) and, unless
+ * Q8_GEMV_MX sets the row groups, at least 24 Mi weights at 4 tokens and 48 Mi at 3 (the pair
+ * counts both matrices). Measured against the VALU kernel on the 2B and 9B shapes: it wins at 4
+ * tokens from 25 Mi weights up (6144x4096: 10.9 against 11.5 us; the pair 12288x4096: 27-29
+ * against 31-32 us) and loses below (4096x4096: 10.4 against 9.4 us); at 3 tokens it wins only
+ * from K = 12288 and the pair up (4096x12288: 16-18 against 18-20 us; 8192x4096: 13.3 against
+ * 12.0 us). */
+bool q8_gemv_mx_takes(long rows, long cols, long t, bool pair)
 {
-    return (t == 3 || t == 4) && mx_choose(rows, cols) > 0;
+    if ((t != 3 && t != 4) || mx_choose(rows, cols) == 0)
+        return false;
+    const char *v = getenv("Q8_GEMV_MX");
+    if (v && atoi(v) > 0)
+        return true;
+    const double weights = (double)rows * (double)cols * (pair ? 2.0 : 1.0);
+    return weights >= (t == 4 ? 24.0 : 48.0) * (double)(1 << 20);
 }
 
 /* groups in flight a wave: 2, and 1 for the pair (its two matrices double the weight registers;
@@ -216,7 +229,7 @@ bool q8_launch_gemv_mx(q8_stream_t stream, const void *w0, const void *w1, long 
 {
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
-    if (!q8_gemv_mx_takes(rows, cols, t) || (w1 && res))
+    if (!q8_gemv_mx_takes(rows, cols, t, w1 != nullptr) || (w1 && res))
         return false;
     if (w1)
         return t == 3 ? mx_go<3, 1, 0>(s, a, b, rows, cols, x, x_stride, y, nullptr) : mx_go<4, 1, 0>(s, a, b, rows, cols, x, x_stride, y, nullptr);

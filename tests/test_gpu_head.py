@@ -112,7 +112,8 @@ def test_draft_head_is_prefix(rt, oracle, head, t):
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (4096, 12288)])
 def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
     """gemm(t)[k] against gemv(x[k]) (src/card/gemm.h:7): bit for bit in the reference-order kernel at
-    every t and in the VALU decode kernel at t = 2; at t = 3, 4 (the matrix-core decode kernel),
+    every t and in the VALU decode kernel at t = 2; at t = 3, 4 (on 4096x12288 the matrix-core decode
+    kernel; 4096x4096 stays on the VALU one),
     at t >= 5 (the matrix-core product) and at every K split tried (1, 3 and the planner's),
     within the parity bar of the one-token product and of F64."""
     h = Handle(rt, rows, cols, seed=rows + cols)
