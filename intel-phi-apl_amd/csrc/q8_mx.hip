@@ -160,11 +160,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_mx(const uint8_t *__restrict__ w
  * the row groups (for tuning sweeps). */
 static int mx_choose(long rows, long cols)
 {
-    static int cached = -2;
-    if (cached == -2) {
-        const char *v = getenv("Q8_GEMV_MX");
-        cached = v ? atoi(v) : -1;
-    }
+    const char *v = getenv("Q8_GEMV_MX"); /* read at every call: tests switch it */
+    const int cached = v ? atoi(v) : -1;
     const long kb = cols % 1024 ? 0 : cols / 1024;
     if (cached == 0 || !(kb == 2 || kb == 4 || kb == 6 || kb == 8 || kb == 12 || kb == 16) || rows % 4)
         return 0;
