@@ -13,17 +13,18 @@ value = algorithmic bytes per token (Q8_0 weights + x read once + y written once
 roofline = the dominant kernel (the fused gate+up): its algorithmic bytes per launch over its
         average duration, from events attached to each of its launches in a timed replay.
 cpu_baseline = the reference's own host path (oracle/_ref: src/card/gemv.c with the team of
-        src/card/team.c, built from the reference's sources) on this host's cores, over one 9B
-        layer's five products; the oracle's own restatement when oracle/_ref is absent. Beside
-        it, under cpu_baseline.configs, the same path on the 4096x4096 GEMV, the M = 16 GEMM and
-        the M = 4 verify products.
+        src/card/team.c, built from the reference's sources with its own host flags) on this
+        host's cores, over one 9B layer's five products; the oracle's own restatement when
+        oracle/_ref is absent. Beside it, under cpu_baseline.configs, the same path on the
+        4096x4096 GEMV, the M = 16 GEMM and the M = 4 verify products, and under
+        cpu_baseline.variants the layer on the build with -mfma added.
 
 Also in the line, each measured with its own weights rotated through >= 512 MB so that the
 256 MB Infinity Cache cannot serve them: the single 4096x4096 GEMV, the draft head (first 32768
 rows), the prompt GEMM at M = 16, 40 and 64, the verify path at M = 2..4 (fused pair + down,
 heavy-tailed scales), the 2B layer set, the DeltaNet quartet as four launches and as one round,
-a 9B layer with its norm and residual epilogues, the host-pointer entry points (PCIe-inclusive)
-and the GGUF load of one 9B layer.
+a 9B layer with its norm and residual epilogues, the host-pointer entry points (PCIe-inclusive),
+the whole 9B token through them, and the GGUF load of one 9B layer.
 """
 import argparse
 import ctypes as c
