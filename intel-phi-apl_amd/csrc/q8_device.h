@@ -75,16 +75,18 @@ __device__ __forceinline__ float q8_wave_sum_dpp(float v)
 /* v[c] of lane j of each quad (lanes 4b..4b+3) <- v[j] of lane c: a 4x4 transpose inside the quad,
  * in two exchanges (lanes j^1, then j^2). Each step is one v_cndmask_b32 whose first operand is
  * read through DPP from the partner lane: out = vcc ? keep : partner's value, with vcc the lanes
- * that keep (lanes whose bit 0, then bit 1, equals that of c). */
+ * that keep (lanes whose bit 0, then bit 1, equals that of c). The two s_mov that set vcc come
+ * first in every step, so a DPP read is at least two instructions after the VALU write of its
+ * operand (the wait states gfx9 requires between them). The lane masks are the same in every
+ * quad, so the step needs no lane index. */
 #define Q8_QT_STEP(out, keep, give, perm, mask)                                                                        \
     asm volatile("s_mov_b32 vcc_lo, " mask "\n\ts_mov_b32 vcc_hi, " mask "\n\tv_cndmask_b32_dpp %0, %1, %2, vcc " perm   \
                  " row_mask:0xf bank_mask:0xf"                                                                         \
                  : "=v"(out)                                                                                           \
                  : "v"(give), "v"(keep)                                                                                \
                  : "vcc")
-__device__ __forceinline__ void q8_quad_transpose(uint32_t (&v)[4], int j)
+__device__ __forceinline__ void q8_quad_transpose(uint32_t (&v)[4])
 {
-    (void)j;
     uint32_t a[4];
     /* c even keeps in lanes with j even (0x5555...), c odd in lanes with j odd (0xaaaa...) */
     Q8_QT_STEP(a[0], v[0], v[1], "quad_perm:[1,0,3,2]", "0x55555555");
@@ -100,12 +102,12 @@ __device__ __forceinline__ void q8_quad_transpose(uint32_t (&v)[4], int j)
 #undef Q8_QT_STEP
 
 /* the same for four 16-byte registers, component by component */
-__device__ __forceinline__ void q8_quad_transpose4(uint4 (&v)[4], int j)
+__device__ __forceinline__ void q8_quad_transpose4(uint4 (&v)[4])
 {
     uint32_t t[4];
 #define Q8_QT(f)                                                                                                       \
     t[0] = v[0].f, t[1] = v[1].f, t[2] = v[2].f, t[3] = v[3].f;                                                        \
-    q8_quad_transpose(t, j);                                                                                           \
+    q8_quad_transpose(t);                                                                                              \
     v[0].f = t[0], v[1].f = t[1], v[2].f = t[2], v[3].f = t[3];
     Q8_QT(x) Q8_QT(y) Q8_QT(z) Q8_QT(w)
 #undef Q8_QT

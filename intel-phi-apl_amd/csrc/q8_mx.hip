@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mx(const uint8_t *__restrict__ w
     /* lane 4b+j: xr[c][h] = token j, floats [64 b + 16 c + 4 h, +4) */
 #pragma unroll
     for (int c = 0; c < 4; c++)
-        q8_quad_transpose4(xr[c], j);
+        q8_quad_transpose4(xr[c]);
 
     __shared__ float red[RGW][NW][4][OUT];
 #pragma unroll
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mx(const uint8_t *__restrict__ w
         q8_f32x4 acc[P];
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            q8_quad_transpose4(q[k][p], j);
+            q8_quad_transpose4(q[k][p]);
             const uint32_t ds = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (16 * j + b), (int)dl[k][p]);
             acc[p] = q8_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll

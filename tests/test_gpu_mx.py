@@ -76,3 +76,54 @@ def test_matrix_core_decode_tall(rt, oracle):
     assert_parity(y, yg, "tall product")
     assert_parity(p, oracle.swiglu_f64(yg, oracle.gemm_f64(q8u, rows, cols, x)), "tall pair")
     assert np.array_equal(z.view(np.uint32), (r + y).view(np.uint32))
+
+
+def test_matrix_core_decode_in_a_graph(rt):
+    """The kernel's products recorded into a graph (the product at 4 tokens, the pair at 3, the
+    residual in place at 4) and replayed three times with eager work between: every replay's bits
+    equal the eager run's."""
+    rows, cols = 128, 4096
+    rng = np.random.default_rng(5)
+    mats = [synth.q8_rows(rng, rows, cols) for _ in range(3)]
+    x = synth.x_f32(rng, 4, cols)
+    r = rng.standard_normal((4, rows)).astype(np.float32)
+    old = os.environ.get("Q8_GEMV_MX")
+    os.environ["Q8_GEMV_MX"] = "2"
+    ws = [rt.upload(m, rows, cols) for m in mats]
+    try:
+        with Dev(rt) as d:
+            dx, dr0, dr = d.put(x), d.put(r), d.empty(4 * 4 * rows)
+            y1, y2 = d.empty(4 * 4 * rows), d.empty(4 * 3 * rows)
+
+            def seq():
+                rt.lib.rt_gemm_dev(rt.R, c.c_void_p(ws[0]), rows, cols, c.c_void_p(dx), cols, 4, c.c_void_p(y1))
+                rt.lib.rt_gemv_swiglu_dev(rt.R, c.c_void_p(ws[1]), c.c_void_p(ws[2]), rows, cols, c.c_void_p(dx), cols, 3, c.c_void_p(y2))
+                rt.lib.rt_gemm_residual_dev(rt.R, c.c_void_p(ws[2]), rows, cols, c.c_void_p(dx), cols, 4, c.c_void_p(dr), c.c_void_p(dr))
+
+            outs = ((y1, (4, rows)), (y2, (3, rows)), (dr, (4, rows)))
+            rt.lib.rt_dev_copy(rt.R, c.c_void_p(dr), c.c_void_p(dr0), 4 * 4 * rows)
+            seq()
+            want = [d.get(p, s, np.float32) for p, s in outs]
+            rt.lib.rt_dev_copy(rt.R, c.c_void_p(dr), c.c_void_p(dr0), 4 * 4 * rows)
+            rt.lib.rt_graph_begin(rt.R)
+            seq()
+            g = rt.lib.rt_graph_end(rt.R)
+            try:
+                for rep in range(3):
+                    rt.lib.rt_dev_copy(rt.R, c.c_void_p(dr), c.c_void_p(dr0), 4 * 4 * rows)
+                    rt.to_dev(y1, np.zeros((4, rows), np.float32))
+                    rt.lib.rt_graph_launch(rt.R, c.c_void_p(g))
+                    got = [d.get(p, s, np.float32) for p, s in outs]
+                    for a, b in zip(got, want):
+                        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {rep}"
+                    seq()  # eager work between the replays
+                    rt.sync()
+            finally:
+                rt.lib.rt_graph_free(rt.R, c.c_void_p(g))
+    finally:
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+        if old is None:
+            os.environ.pop("Q8_GEMV_MX", None)
+        else:
+            os.environ["Q8_GEMV_MX"] = old
