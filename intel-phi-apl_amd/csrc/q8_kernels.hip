@@ -388,6 +388,11 @@ static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *
     int rw = pair ? (mt == 2 || mt == 3 ? 8 : 4) : 8, nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
+    /* 2 tokens at K = 12288: 8 rows take 88 registers, so one 12-wave workgroup fits a CU and
+     * the grid runs in two rounds; 16 rows (129 registers, still one a CU) run in one, 4 % faster
+     * on 4096 x 12288 */
+    if (!pair && mt == 2 && nw == 12 && rows / 16 >= 256)
+        rw = 16;
     /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
      * SIMD) stream */
     while (rw > 2 && rows / rw * nw < 2048)
