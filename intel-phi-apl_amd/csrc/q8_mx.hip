@@ -19,11 +19,11 @@ typedef float q8_f32x4 __attribute__((ext_vector_type(4)));
  *
  * Workgroup: NW waves, RGW groups of 4 rows, all of K = 1024*NW; wave w takes columns
  * [1024 w, +1024), lane 4b+j the 64 columns [1024 w + 64 b, +64). x is loaded once and kept in
- * registers; the row groups then stream through NB register buffers: the loads of group n+NB
- * are issued as soon as group n is computed, so each wave keeps NB groups in flight and computes
- * every group while later ones are still arriving (with all of a wave's loads issued at once,
- * every wave's last load lands near the end and the arithmetic runs after the memory instead of
- * under it).
+ * registers; the weights then stream in steps of one matrix's 4 rows (the pair's gate and up of a
+ * row group are two steps) through NB register buffers: the loads of step s+NB are issued as soon
+ * as step s is computed, so each wave keeps NB steps in flight and computes every step while later
+ * ones are still arriving (with all of a wave's loads issued at once, every wave's last load
+ * lands near the end and the arithmetic runs after the memory instead of under it).
  *
  * The loads do not follow the lane layout: a quad holding four rows (or tokens) at one column
  * would touch four cache lines per quad and load, so each load reads 16 contiguous bytes a lane
@@ -62,22 +62,25 @@ __global__ __launch_bounds__(64 * NW) void gemv_mx(const uint8_t *__restrict__ w
 #pragma unroll
         for (int h = 0; h < 4; h++)
             xr[c][h] = h < MT ? *(const uint4 *)(x + h * x_stride + c0 + 64 * b + 16 * c + 4 * j) : make_uint4(0u, 0u, 0u, 0u);
-    /* weights of group n: load (p, r) is row 4n + r, bytes [64 b + 16 j, +16) of the wave's
-     * columns; lane L: the dword L & 15 (blocks 2(L & 15), +1) of row 4n + (L >> 4)'s 32 scales
-     * here */
-    uint4 q[NB][P][4];
-    uint32_t dl[NB][P];
-#define Q8_MX_LOAD(n, k)                                                                                               \
-    _Pragma("unroll") for (int p = 0; p < P; p++)                                                                      \
+    /* the weights stream in steps: step s is matrix s % P of row group s / P (the pair's gate and
+     * up of a group are two steps), through NB register buffers, the loads of step s + NB issued as
+     * soon as step s is computed. Load r of a step is row 4n + r, bytes [64 b + 16 j, +16) of the
+     * wave's columns; lane L: the dword L & 15 (blocks 2(L & 15), +1) of row 4n + (L >> 4)'s 32
+     * scales here */
+    constexpr int ST = RGW * P;
+    uint4 q[NB][4];
+    uint32_t dl[NB];
+#define Q8_MX_LOAD(s, k)                                                                                               \
     {                                                                                                                  \
-        const uint8_t *w = p ? w1 : w0;                                                                                \
-        _Pragma("unroll") for (int r = 0; r < 4; r++) q[k][p][r] =                                                     \
-            *(const uint4 *)(w + q8s_row_q(r0 + 4 * (n) + r, cols) + c0 + 64 * b + 16 * j);                             \
-        dl[k][p] = *(const uint32_t *)(w + q8s_row_d(r0 + 4 * (n) + (lane >> 4), cols) + 2 * (c0 / 32) + 4 * (lane & 15)); \
+        const int n_ = (s) / P;                                                                                        \
+        const uint8_t *w = (s) % P ? w1 : w0;                                                                          \
+        _Pragma("unroll") for (int r = 0; r < 4; r++) q[k][r] =                                                        \
+            *(const uint4 *)(w + q8s_row_q(r0 + 4 * n_ + r, cols) + c0 + 64 * b + 16 * j);                              \
+        dl[k] = *(const uint32_t *)(w + q8s_row_d(r0 + 4 * n_ + (lane >> 4), cols) + 2 * (c0 / 32) + 4 * (lane & 15));  \
     }
 #pragma unroll
-    for (int n = 0; n < NB && n < RGW; n++) {
-        Q8_MX_LOAD(n, n)
+    for (int s = 0; s < NB && s < ST; s++) {
+        Q8_MX_LOAD(s, s)
     }
     /* keep the loads where they are: left to itself the scheduler sinks them between the MFMAs to
      * save registers, and each wait then costs a memory round trip */
@@ -89,47 +92,46 @@ __global__ __launch_bounds__(64 * NW) void gemv_mx(const uint8_t *__restrict__ w
         q8_quad_transpose4(xr[c]);
 
     __shared__ float red[RGW][NW][4][OUT];
+    q8_f32x4 acc[P];
 #pragma unroll
-    for (int n = 0; n < RGW; n++) {
-        const int k = n % NB;
-        /* lane 4b+j: q[k][p][r] = row 4n + j, bytes [64 b + 16 r, +16); ds = the scales of blocks
+    for (int s = 0; s < ST; s++) {
+        const int k = s % NB, n = s / P, p = s % P;
+        /* lane 4b+j: q[k][r] = row 4n + j, bytes [64 b + 16 r, +16); ds = the scales of blocks
          * 2b, 2b+1 of row 4n + j (from lane 16 j + b) */
-        q8_f32x4 acc[P];
+        q8_quad_transpose4(q[k]);
+        const uint32_t ds = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (16 * j + b), (int)dl[k]);
+        acc[p] = q8_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int p = 0; p < P; p++) {
-            q8_quad_transpose4(q[k][p]);
-            const uint32_t ds = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (16 * j + b), (int)dl[k][p]);
-            acc[p] = q8_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < 4; r++) {
+            const uint32_t qw[4] = {q[k][r].x, q[k][r].y, q[k][r].z, q[k][r].w};
+            const uint32_t xw[16] = {xr[r][0].x, xr[r][0].y, xr[r][0].z, xr[r][0].w, xr[r][1].x, xr[r][1].y, xr[r][1].z, xr[r][1].w,
+                                     xr[r][2].x, xr[r][2].y, xr[r][2].z, xr[r][2].w, xr[r][3].x, xr[r][3].y, xr[r][3].z, xr[r][3].w};
+            q8_f32x4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t qw[4] = {q[k][p][r].x, q[k][p][r].y, q[k][p][r].z, q[k][p][r].w};
-                const uint32_t xw[16] = {xr[r][0].x, xr[r][0].y, xr[r][0].z, xr[r][0].w, xr[r][1].x, xr[r][1].y, xr[r][1].z, xr[r][1].w,
-                                         xr[r][2].x, xr[r][2].y, xr[r][2].z, xr[r][2].w, xr[r][3].x, xr[r][3].y, xr[r][3].z, xr[r][3].w};
-                q8_f32x4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int e = 0; e < 16; e++)
+                dv = __builtin_amdgcn_mfma_f32_4x4x1f32(__builtin_bit_cast(float, xw[e]), q8_s8(qw[e >> 2], e & 3), dv, 0, 0, 0);
+            const float d = q8_half((uint16_t)(ds >> (16 * (r >> 1))));
 #pragma unroll
-                for (int e = 0; e < 16; e++)
-                    dv = __builtin_amdgcn_mfma_f32_4x4x1f32(__builtin_bit_cast(float, xw[e]), q8_s8(qw[e >> 2], e & 3), dv, 0, 0, 0);
-                const float d = q8_half((uint16_t)(ds >> (16 * (r >> 1))));
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[p][i] = __builtin_fmaf(dv[i], d, acc[p][i]);
-            }
+            for (int i = 0; i < 4; i++)
+                acc[p][i] = __builtin_fmaf(dv[i], d, acc[p][i]);
         }
-        /* over b within each row of 16 lanes: (v + ror 8) + ror 4 of that, every lane the sum of
-         * the four lanes of its j; lanes 16R + j (R = 0..3) keep it for the LDS sum */
+        if (p == P - 1) {
+            /* over b within each row of 16 lanes: (v + ror 8) + ror 4 of that, every lane the sum
+             * of the four lanes of its j; lanes 16R + j (R = 0..3) keep it for the LDS sum */
 #pragma unroll
-        for (int p = 0; p < P; p++)
+            for (int pp = 0; pp < P; pp++)
 #pragma unroll
-            for (int i = 0; i < MT; i++) {
-                float v = acc[p][i];
-                v += Q8_DPP(v, 0x128); /* row_ror:8 */
-                v += Q8_DPP(v, 0x124); /* row_ror:4 */
-                if ((lane & 12) == 0)
-                    red[n][wave][lane >> 4][(p * 4 + j) * MT + i] = v;
-            }
-        if (n + NB < RGW) {
+                for (int i = 0; i < MT; i++) {
+                    float v = acc[pp][i];
+                    v += Q8_DPP(v, 0x128); /* row_ror:8 */
+                    v += Q8_DPP(v, 0x124); /* row_ror:4 */
+                    if ((lane & 12) == 0)
+                        red[n][wave][lane >> 4][(pp * 4 + j) * MT + i] = v;
+                }
+        }
+        if (s + NB < ST) {
             __builtin_amdgcn_sched_barrier(0);
-            Q8_MX_LOAD(n + NB, k)
+            Q8_MX_LOAD(s + NB, k)
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -192,12 +194,11 @@ bool q8_gemv_mx_takes(long rows, long cols, long t, bool pair)
     return weights >= (t == 4 ? 24.0 : 48.0) * (double)(1 << 20);
 }
 
-/* groups in flight a wave: 2, and 1 for the pair (its two matrices double the weight registers;
- * with 2 it fits 2 waves a SIMD, with 1 three) */
+/* steps in flight a wave: 2 (the pair's gate and up of a row group, or two row groups) */
 template <int MT, int PAIR, int RGW, int EPI>
 static bool mx_go_nw(hipStream_t s, long kb, const uint8_t *a, const uint8_t *b, long rows, long cols, const float *x, long xs, float *y, const float *res)
 {
-    constexpr int NB = PAIR ? 1 : 2;
+    constexpr int NB = 2;
 #define K1(N)                                                                                                          \
     if (kb == N) {                                                                                                     \
         Q8_LAUNCH(q8_time_name("gemv_mx", 6, MT, N, PAIR, RGW, NB, EPI), (gemv_mx<MT, N, PAIR, RGW, NB, EPI>), dim3((unsigned)(rows / (4 * RGW))),      \
