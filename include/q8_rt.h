@@ -136,9 +136,9 @@ void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float 
  * two runtimes) race. */
 void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* A round of n (1..RT_BATCH) products sharing x, none reading another's y: y[i] = X w[i]^T,
- * w[i] [rows[i] cols], as one launch where the kernel takes the shape (t <= 4; at t = 3 and 4 not
- * when a product's shape goes to the matrix-core decode kernel, so that each product's bits are
- * its own launch's), else one after another. The device form of rt_gemv_q x n + rt_gemv_go, which
+ * w[i] [rows[i] cols], as one launch where the kernel takes the shape (t <= 4; not while the
+ * environment variable Q8_GEMV_MX sends 3 and 4 tokens to the matrix-core decode kernel, so that
+ * each product's bits are its own launch's), else one after another. The device form of rt_gemv_q x n + rt_gemv_go, which
  * uses the same launch for queued decode products that share x (the DeltaNet quartet
  * QKV/GATE/BETA/ALPHA, src/apl/qwen35.apl:93-96). */
 void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
@@ -148,9 +148,9 @@ void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows,
 /* ---- the epilogues on either side of a product (additions; the reference computes them on its
  * host around the products: RMS = {⍺×⍵×(RMS_EPS+(+/⍵×⍵)÷≢⍵)*¯0.5}, src/apl/qwen35.apl:49, before a
  * layer's mixer and FFN, and the residual Z←X+… after them, qwen35.apl:131-139). Fused into the
- * decode kernel (t <= 4) for K = 2048, 4096, 6144 and 12288, the residual into the matrix-core
- * decode kernel's store at t = 3, 4 and the matrix-core product's for t >= 5; other shapes run
- * the norm or the add as a kernel of its own. The
+ * decode kernel (t <= 4) for K = 2048, 4096, 6144 and 12288 (the residual into the matrix-core
+ * decode kernel's store when Q8_GEMV_MX selects it at t = 3, 4) and the residual into the
+ * matrix-core product's for t >= 5; other shapes run the norm or the add as a kernel of its own. The
  * norm is s = 1 / sqrt(eps + sum_k x[k]^2 / cols) per token in F32, xn[k] = nw[k] * (x[k] * s); its
  * sum runs in a fixed order for a given shape, so results repeat bit for bit, and a fused and a
  * separate norm differ only by that order (an ulp or so of s). The residual is one F32 add of the
@@ -229,7 +229,7 @@ float rt_timer_stop(struct rt *R);
  * duration in microseconds, its name as rocprof prints it (64 bytes each in names, NUL-padded;
  * names may be NULL) and its grid in threads (grid may be NULL); reading clears the records.
  * rt_ktime(R, 1) also clears. */
-#define RT_K_GEMV 0      /* t <= 4, the decode kernels (VALU; at t = 3, 4 the matrix-core one where it takes the shape) */
+#define RT_K_GEMV 0      /* t <= 4, the decode kernels (VALU; at t = 3, 4 the matrix-core one where Q8_GEMV_MX selects it) */
 #define RT_K_GEMV_PAIR 1 /* the fused gate/up pair, t <= 4 */
 #define RT_K_GEMM 2      /* t >= 5, the matrix-core kernel */
 #define RT_K_GEMM_PAIR 3

@@ -72,6 +72,98 @@ __device__ __forceinline__ float q8_wave_sum_dpp(float v)
     return (r0 + r1) + (r2 + r3);
 }
 
+/* the least power of two >= n (n >= 1) */
+__host__ __device__ constexpr int q8_pow2ceil(int n)
+{
+    return n <= 1 ? 1 : 2 * q8_pow2ceil((n + 1) / 2);
+}
+
+/* The sums over the 64 lanes of V values a lane (V a power of two), by a butterfly over the lane
+ * bits 5, 4, 3 and then 0, 1, 2: the same lane pairs in the same order for every V, so a value's
+ * sum has the same bits whatever V is. While two or more values are left, a step over bit 5, 4 or
+ * 3 is transposed: lanes with the bit clear keep the first half of the values and the others the
+ * second half, each adding its partner's copy of the values it keeps, so a step costs one add a
+ * kept value instead of one a value. A single value is summed in place. Bit 5 pairs lanes with
+ * v_permlane32_swap (the upper 32 lanes of its first operand trade places with the lower 32 of
+ * its second), bit 4 with v_permlane16_swap (the odd rows of 16 lanes of the first with the even
+ * rows of the second), bit 3 with DPP row_ror:8; bits 0, 1, 2 within each group of 8 lanes with
+ * DPP quad_perm [1,0,3,2], [2,3,0,1] and row_half_mirror (exact pairs once each quad holds equal
+ * values). On return, with T = min(3, log2 V) transposed steps, v[k] (k < V >> T) of lane l is the
+ * sum of value q8_wave_sums_index<V>(l, k); lanes with q8_wave_sums_owner<V>(l) hold each value
+ * once. The two results of a swap pass through q8_swap_sum, which hides the second from the
+ * optimiser: summed directly, this compiler folds their sum into twice the first result (checked
+ * in its gfx950 assembly: v_permlane32_swap_b32 v1, v2 then v_add_f32 v1, v1, v1). */
+__device__ __forceinline__ float q8_swap_sum(uint32_t a, uint32_t b)
+{
+    asm volatile("" : "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+template <int V>
+__device__ __forceinline__ constexpr int q8_wave_sums_steps()
+{
+    return V >= 8 ? 3 : V >= 4 ? 2 : V >= 2 ? 1 : 0;
+}
+template <int V>
+__device__ __forceinline__ int q8_wave_sums_index(int l, int k)
+{
+    constexpr int T = q8_wave_sums_steps<V>();
+    return (T > 0 && (l & 32) ? V / 2 : 0) + (T > 1 && (l & 16) ? V / 4 : 0) + (T > 2 && (l & 8) ? V / 8 : 0) + k;
+}
+template <int V>
+__device__ __forceinline__ bool q8_wave_sums_owner(int l)
+{
+    constexpr int T = q8_wave_sums_steps<V>();
+    return (l & 7) == 0 && (T > 2 || !(l & 8)) && (T > 1 || !(l & 16)) && (T > 0 || !(l & 32));
+}
+template <int V>
+__device__ __forceinline__ void q8_wave_sums(float (&v)[V], int lane)
+{
+    static_assert((V & (V - 1)) == 0, "a power of two");
+    /* bit 5 */
+    if constexpr (V >= 2) {
+#pragma unroll
+        for (int i = 0; i < V / 2; i++) {
+            const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v[i]), __builtin_bit_cast(uint32_t, v[i + V / 2]), false, false);
+            v[i] = q8_swap_sum(s[0], s[1]);
+        }
+    } else {
+        const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[0]), false, false);
+        v[0] = q8_swap_sum(s[0], s[1]);
+    }
+    constexpr int N4 = V >= 2 ? V / 2 : 1; /* values left */
+    /* bit 4 */
+    if constexpr (N4 >= 2) {
+#pragma unroll
+        for (int i = 0; i < N4 / 2; i++) {
+            const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v[i]), __builtin_bit_cast(uint32_t, v[i + N4 / 2]), false, false);
+            v[i] = q8_swap_sum(s[0], s[1]);
+        }
+    } else {
+        const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[0]), false, false);
+        v[0] = q8_swap_sum(s[0], s[1]);
+    }
+    constexpr int N3 = N4 >= 2 ? N4 / 2 : 1;
+    /* bit 3 */
+    if constexpr (N3 >= 2) {
+        const bool hi = (lane & 8) != 0;
+#pragma unroll
+        for (int i = 0; i < N3 / 2; i++) {
+            const float keep = hi ? v[i + N3 / 2] : v[i], give = hi ? v[i] : v[i + N3 / 2];
+            v[i] = keep + Q8_DPP(give, 0x128); /* row_ror:8 */
+        }
+    } else {
+        v[0] += Q8_DPP(v[0], 0x128);
+    }
+    constexpr int N = N3 >= 2 ? N3 / 2 : 1;
+    /* bits 0, 1, 2 */
+#pragma unroll
+    for (int k = 0; k < N; k++) {
+        v[k] += Q8_DPP(v[k], 0xb1);  /* quad_perm [1,0,3,2] */
+        v[k] += Q8_DPP(v[k], 0x4e);  /* quad_perm [2,3,0,1] */
+        v[k] += Q8_DPP(v[k], 0x141); /* row_half_mirror */
+    }
+}
+
 /* v[c] of lane j of each quad (lanes 4b..4b+3) <- v[j] of lane c: a 4x4 transpose inside the quad,
  * in two exchanges (lanes j^1, then j^2). Each step is one v_cndmask_b32 whose first operand is
  * read through DPP from the partner lane: out = vcc ? keep : partner's value, with vcc the lanes

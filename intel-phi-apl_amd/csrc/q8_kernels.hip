@@ -239,27 +239,10 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
                     acc[r][p][m] = __builtin_fmaf(sum, q8_half(dh[r][p][s]), acc[r][p][m]);
                 }
             }
-    if (NW == 1) {
-#pragma unroll
-        for (int r = 0; r < RW; r++)
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                float v[P];
-#pragma unroll
-                for (int p = 0; p < P; p++) {
-                    v[p] = q8_wave_sum_dpp(acc[r][p][m]);
-                    if constexpr (EPI == 1)
-                        v[p] *= 1.0f / sqrtf(e.eps + ss[m] / (float)cols);
-                }
-                if (lane == 0) {
-                    const long i = m * rows + r0 + r;
-                    const float o = PAIR ? q8_swiglu(v[0], v[P - 1]) : v[0];
-                    y[i] = EPI == 2 ? e.res[i] + o : o;
-                }
-            }
-        return;
-    }
-    __shared__ float red[NW][RW * P * MT];
+    /* the wave's RW*P*MT sums over its lanes (q8_wave_sums, padded to a power of two), each
+     * written to LDS once; then the NW waves' in wave order */
+    constexpr int V = RW * P * MT, VP = q8_pow2ceil(V);
+    __shared__ float red[NW][V];
     __shared__ float nsum[EPI == 1 ? NW : 1][MT];
     if constexpr (EPI == 1) {
         if (lane == 0)
@@ -267,16 +250,26 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
             for (int m = 0; m < MT; m++)
                 nsum[wave][m] = ss[m];
     }
+    float vals[VP];
 #pragma unroll
     for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int m = 0; m < MT; m++) {
-                const float v = q8_wave_sum_dpp(acc[r][p][m]);
-                if (lane == 0)
-                    red[wave][(r * P + p) * MT + m] = v;
-            }
+            for (int m = 0; m < MT; m++)
+                vals[(r * P + p) * MT + m] = acc[r][p][m];
+#pragma unroll
+    for (int i = V; i < VP; i++)
+        vals[i] = 0.0f;
+    q8_wave_sums<VP>(vals, lane);
+    if (q8_wave_sums_owner<VP>(lane)) {
+#pragma unroll
+        for (int k = 0; k < (VP >> q8_wave_sums_steps<VP>()); k++) {
+            const int g = q8_wave_sums_index<VP>(lane, k);
+            if (g < V)
+                red[wave][g] = vals[k];
+        }
+    }
     __syncthreads();
     if (threadIdx.x < RW * MT) {
         const int r = threadIdx.x / MT, m = threadIdx.x % MT;
@@ -382,16 +375,16 @@ static bool gemv_go_rw(hipStream_t s, int nw, long kb, const uint8_t *a, const u
 /* The decode kernel's rows a workgroup (rw) and waves (nw) for a shape; kb = cols / 1024 */
 static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *nw_out)
 {
-    /* measured on the 9B shapes: 8 rows a workgroup (4 for the pair: the same 8 rows of loads a
-     * lane; 8 for the pair at 2 and 3 tokens, 5 % faster there and 7 % slower at 1 and 4), one
-     * 1024-column step a wave, so K = 4096 takes 4 waves and K = 12288 takes 12 */
-    int rw = pair ? (mt == 2 || mt == 3 ? 8 : 4) : 8, nw = (int)kb;
+    /* measured on the 9B shapes: 8 rows a workgroup (for the pair 4 at 1 and 3 tokens, the same
+     * 8 rows of loads a lane, and 8 at 2 and 4), one 1024-column step a wave, so K = 4096 takes 4
+     * waves and K = 12288 takes 12 */
+    int rw = pair ? (mt == 2 || mt == 4 ? 8 : 4) : 8, nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
-    /* 2 tokens at K = 12288: 8 rows take 88 registers, so one 12-wave workgroup fits a CU and
-     * the grid runs in two rounds; 16 rows (129 registers, still one a CU) run in one, 4 % faster
-     * on 4096 x 12288 */
-    if (!pair && mt == 2 && nw == 12 && rows / 16 >= 256)
+    /* 2 and 4 tokens at K = 12288: 16 rows, one 12-wave workgroup a CU and the grid in one round
+     * (4096 x 12288: 11.4 against 12.3 us at 2 tokens, 14.5 against 16.2 at 4; at 3 tokens 16
+     * rows spill) */
+    if (!pair && (mt == 2 || mt == 4) && nw == 12 && rows / 16 >= 256)
         rw = 16;
     /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
      * SIMD) stream */

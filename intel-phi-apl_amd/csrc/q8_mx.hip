@@ -158,8 +158,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_mx(const uint8_t *__restrict__ w
  * the shape: K a multiple of 1024 with 2, 4, 6, 8, 12 or 16 waves, rows a multiple of 4. The
  * largest of 4, 2, 1 that divides the row groups and leaves at least 3072 waves (3 a SIMD), else
  * 1. Measured on the 9B shapes: 4 for the gate+up pair (768 workgroups of 4 waves) and for down
- * (256 of 12). Q8_GEMV_MX = "0" leaves 3 and 4 tokens on the VALU kernel; "1", "2" or "4" sets
- * the row groups (for tuning sweeps). */
+ * (256 of 12). Q8_GEMV_MX = "1", "2" or "4" sends 3 and 4 tokens here with that many row
+ * groups (for measuring it against the VALU kernel); unset or "0", they stay on the VALU kernel. */
 static int mx_choose(long rows, long cols)
 {
     const char *v = getenv("Q8_GEMV_MX"); /* read at every call: tests switch it */
@@ -176,22 +176,19 @@ static int mx_choose(long rows, long cols)
     return 1;
 }
 
-/* Whether the kernel takes t tokens of a product: a shape it runs (mx_choose) and, unless
- * Q8_GEMV_MX sets the row groups, at least 24 Mi weights at 4 tokens and 48 Mi at 3 (the pair
- * counts both matrices). Measured against the VALU kernel on the 2B and 9B shapes: it wins at 4
- * tokens from 25 Mi weights up (6144x4096: 10.9 against 11.5 us; the pair 12288x4096: 27-29
- * against 31-32 us) and loses below (4096x4096: 10.4 against 9.4 us); at 3 tokens it wins only
- * from K = 12288 and the pair up (4096x12288: 16-18 against 18-20 us; 8192x4096: 13.3 against
- * 12.0 us). */
+/* Whether the kernel takes t tokens of a product: a shape it runs (mx_choose), and only when
+ * Q8_GEMV_MX sets the row groups. The VALU decode kernel, its lanes summed by q8_wave_sums, is
+ * as fast or faster at every 9B shape measured at 3 and 4 tokens (4096x12288: 14.7 / 14.4 against
+ * 16.2 / 16.8 us; the pair 12288x4096: 24.4 / 25.3 against 27.2 / 28.5; 6144x4096: 8.6 / 9.0
+ * against 12.0 / 11.6; 151936x4096: 141 / 163 against 141 / 169), and keeps each token's bits
+ * those of its one-token product. */
 bool q8_gemv_mx_takes(long rows, long cols, long t, bool pair)
 {
+    (void)pair;
     if ((t != 3 && t != 4) || mx_choose(rows, cols) == 0)
         return false;
     const char *v = getenv("Q8_GEMV_MX");
-    if (v && atoi(v) > 0)
-        return true;
-    const double weights = (double)rows * (double)cols * (pair ? 2.0 : 1.0);
-    return weights >= (t == 4 ? 24.0 : 48.0) * (double)(1 << 20);
+    return v && atoi(v) > 0;
 }
 
 /* steps in flight a wave: 2 (the pair's gate and up of a row group, or two row groups) */

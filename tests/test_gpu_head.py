@@ -6,10 +6,9 @@
   - DraftLogits (qwen35.apl:170-172): the first 32768 rows of the same handle equal the first
     32768 outputs of the full product bit for bit;
   - the reference keeps gemm(t)[k] == gemv(x[k]) bit for bit (src/card/gemm.h:7). Here the
-    reference-order kernel keeps it, the VALU decode kernel (t <= 2) keeps it, and the matrix-core
-    kernels (the decode one at t = 3, 4; the product at t >= 5, any K split) do not: their outputs
-    differ from the one-token product's by the F32 rounding of another summation order, bounded
-    here by the parity bar.
+    reference-order kernel keeps it, the decode kernel (t <= 4) keeps it, and the matrix-core
+    product (t >= 5, any K split) does not: its outputs differ from the one-token product's by the
+    F32 rounding of another summation order, bounded here by the parity bar.
 """
 import ctypes as c
 import os
@@ -112,10 +111,10 @@ def test_draft_head_is_prefix(rt, oracle, head, t):
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (4096, 12288)])
 def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
     """gemm(t)[k] against gemv(x[k]) (src/card/gemm.h:7): bit for bit in the reference-order kernel at
-    every t and in the VALU decode kernel at t = 2; at t = 3, 4 (on 4096x12288 the matrix-core decode
-    kernel; 4096x4096 stays on the VALU one),
-    at t >= 5 (the matrix-core product) and at every K split tried (1, 3 and the planner's),
-    within the parity bar of the one-token product and of F64."""
+    every t and in the decode kernel at t = 2, 3, 4 (16 rows a workgroup at 2 and 4 tokens on
+    4096x12288, 8 at 1 and 3: the rows a workgroup do not change a row's sums); at t >= 5 (the
+    matrix-core product) and at every K split tried (1, 3 and the planner's), within the parity bar
+    of the one-token product and of F64."""
     h = Handle(rt, rows, cols, seed=rows + cols)
     try:
         X = np.random.default_rng(rows ^ cols).standard_normal((40, cols), dtype=np.float32)
@@ -123,8 +122,9 @@ def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
         one_exact = np.concatenate([h.product(X[k], exact=True) for k in range(8)])
         f64 = oracle.gemm_f64(h.q8, rows, cols, X)
         assert_parity(one, f64, "gemv per token")
-        y = h.product(X[:2])
-        assert np.array_equal(y.view(np.uint32), one[:2].view(np.uint32)), "decode kernel t=2"
+        for t in (2, 3, 4):
+            y = h.product(X[:t])
+            assert np.array_equal(y.view(np.uint32), one[:t].view(np.uint32)), f"decode kernel t={t}"
         for t in (3, 8):
             y = h.product(X[:t], exact=True)
             assert np.array_equal(y.view(np.uint32), one_exact[:t].view(np.uint32)), f"reference order t={t}"
