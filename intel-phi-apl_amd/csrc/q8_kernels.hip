@@ -218,31 +218,17 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
             ss[m] = q8_wave_sum_dpp(a);
         }
     }
-    float acc[RW][P][MT];
-#pragma unroll
-    for (int r = 0; r < RW; r++)
-#pragma unroll
-        for (int p = 0; p < P; p++)
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                acc[r][p][m] = 0.0f;
-#pragma unroll
-                for (int s = 0; s < S; s++) {
-                    const uint32_t qw[4] = {q[r][p][s].x, q[r][p][s].y, q[r][p][s].z, q[r][p][s].w};
-                    const float xs[16] = {xv[m][s][0].x, xv[m][s][0].y, xv[m][s][0].z, xv[m][s][0].w, xv[m][s][1].x, xv[m][s][1].y,
-                                          xv[m][s][1].z, xv[m][s][1].w, xv[m][s][2].x, xv[m][s][2].y, xv[m][s][2].z, xv[m][s][2].w,
-                                          xv[m][s][3].x, xv[m][s][3].y, xv[m][s][3].z, xv[m][s][3].w};
-                    float sum = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 16; j++)
-                        sum = __builtin_fmaf(q8_s8(qw[j >> 2], j & 3), xs[j], sum);
-                    acc[r][p][m] = __builtin_fmaf(sum, q8_half(dh[r][p][s]), acc[r][p][m]);
-                }
-            }
     /* the wave's RW*P*MT sums over its lanes (q8_wave_sums, padded to a power of two), each
-     * written to LDS once; then the NW waves' in wave order */
-    constexpr int V = RW * P * MT, VP = q8_pow2ceil(V);
-    __shared__ float red[NW][V];
+     * written to LDS once; then the NW waves' in wave order. CH: in chunks of up to 8 rows, each
+     * chunk's sums run while later rows' loads still arrive. The two forms give the same bits; the
+     * compiler allocates their registers differently, and each was measured where it is used:
+     * chunks for the pair at 2 tokens (20.0 against 21.2 us on 12288x4096) and for 16 rows at 3
+     * tokens (119 registers, where one block of sums spills: 13.7 against 14.4 us at 8 rows on
+     * 4096x12288); one block everywhere else (the pair at 1 token 18.0 against 18.5 us, 16 rows at
+     * 2 and 4 tokens 11.7 / 14.5 against 12.5 / 15.6). */
+    constexpr bool CH = (PAIR && MT == 2) || (MT == 3 && RW == 16);
+    constexpr int RC = CH && RW > 8 ? 8 : RW, VC = RC * P * MT, VP = q8_pow2ceil(VC);
+    __shared__ float red[NW][RW * P * MT];
     __shared__ float nsum[EPI == 1 ? NW : 1][MT];
     if constexpr (EPI == 1) {
         if (lane == 0)
@@ -250,25 +236,69 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
             for (int m = 0; m < MT; m++)
                 nsum[wave][m] = ss[m];
     }
-    float vals[VP];
+    /* row r's sum of token m of matrix p over the lane's columns */
+    auto row_sum = [&](int r, int p, int m) {
+        float acc = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RW; r++)
+        for (int s = 0; s < S; s++) {
+            const uint32_t qw[4] = {q[r][p][s].x, q[r][p][s].y, q[r][p][s].z, q[r][p][s].w};
+            const float xs[16] = {xv[m][s][0].x, xv[m][s][0].y, xv[m][s][0].z, xv[m][s][0].w, xv[m][s][1].x, xv[m][s][1].y,
+                                  xv[m][s][1].z, xv[m][s][1].w, xv[m][s][2].x, xv[m][s][2].y, xv[m][s][2].z, xv[m][s][2].w,
+                                  xv[m][s][3].x, xv[m][s][3].y, xv[m][s][3].z, xv[m][s][3].w};
+            float sum = 0.0f;
 #pragma unroll
-        for (int p = 0; p < P; p++)
-#pragma unroll
-            for (int m = 0; m < MT; m++)
-                vals[(r * P + p) * MT + m] = acc[r][p][m];
-#pragma unroll
-    for (int i = V; i < VP; i++)
-        vals[i] = 0.0f;
-    q8_wave_sums<VP>(vals, lane);
-    if (q8_wave_sums_owner<VP>(lane)) {
-#pragma unroll
-        for (int k = 0; k < (VP >> q8_wave_sums_steps<VP>()); k++) {
-            const int g = q8_wave_sums_index<VP>(lane, k);
-            if (g < V)
-                red[wave][g] = vals[k];
+            for (int j = 0; j < 16; j++)
+                sum = __builtin_fmaf(q8_s8(qw[j >> 2], j & 3), xs[j], sum);
+            acc = __builtin_fmaf(sum, q8_half(dh[r][p][s]), acc);
         }
+        return acc;
+    };
+    /* a block of VC sums (rows [ch*RC, +RC)) over the lanes, into LDS */
+    auto lane_sums = [&](float (&vals)[VP], int ch) {
+#pragma unroll
+        for (int i = VC; i < VP; i++)
+            vals[i] = 0.0f;
+        q8_wave_sums<VP>(vals, lane);
+        if (q8_wave_sums_owner<VP>(lane)) {
+#pragma unroll
+            for (int k = 0; k < (VP >> q8_wave_sums_steps<VP>()); k++) {
+                const int g = q8_wave_sums_index<VP>(lane, k);
+                if (g < VC)
+                    red[wave][ch * VC + g] = vals[k];
+            }
+        }
+    };
+    if constexpr (CH) {
+#pragma unroll
+        for (int ch = 0; ch < RW / RC; ch++) {
+            float vals[VP];
+#pragma unroll
+            for (int rr = 0; rr < RC; rr++)
+#pragma unroll
+                for (int p = 0; p < P; p++)
+#pragma unroll
+                    for (int m = 0; m < MT; m++)
+                        vals[(rr * P + p) * MT + m] = row_sum(ch * RC + rr, p, m);
+            lane_sums(vals, ch);
+        }
+    } else {
+        float acc[RW][P][MT];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int p = 0; p < P; p++)
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+                    acc[r][p][m] = row_sum(r, p, m);
+        float vals[VP];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int p = 0; p < P; p++)
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+                    vals[(r * P + p) * MT + m] = acc[r][p][m];
+        lane_sums(vals, 0);
     }
     __syncthreads();
     if (threadIdx.x < RW * MT) {
@@ -381,10 +411,10 @@ static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *
     int rw = pair ? (mt == 2 || mt == 4 ? 8 : 4) : 8, nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
-    /* 2 and 4 tokens at K = 12288: 16 rows, one 12-wave workgroup a CU and the grid in one round
-     * (4096 x 12288: 11.4 against 12.3 us at 2 tokens, 14.5 against 16.2 at 4; at 3 tokens 16
-     * rows spill) */
-    if (!pair && (mt == 2 || mt == 4) && nw == 12 && rows / 16 >= 256)
+    /* 2 to 4 tokens at K = 12288: 16 rows, one 12-wave workgroup a CU and the grid in one round
+     * (4096 x 12288: 11.4 against 12.3 us at 2 tokens, 13.7 against 14.4 at 3, 14.5 against 16.2
+     * at 4) */
+    if (!pair && mt >= 2 && nw == 12 && rows / 16 >= 256)
         rw = 16;
     /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
      * SIMD) stream */
