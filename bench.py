@@ -24,7 +24,8 @@ Also in the line, each measured with its own weights rotated through >= 512 MB s
 rows), the prompt GEMM at M = 16, 40 and 64, the verify path at M = 2..4 (fused pair + down,
 heavy-tailed scales), the 2B layer set, the DeltaNet quartet as four launches and as one round,
 a 9B layer with its norm and residual epilogues, the host-pointer entry points (PCIe-inclusive),
-the whole 9B token through them, and the GGUF load of one 9B layer.
+the whole 9B token through them, and the GGUF load of one 9B layer. Each of these runs in a process
+of its own before the token, on fresh device memory as the token's weights are.
 """
 import argparse
 import ctypes as c
@@ -32,6 +33,7 @@ import importlib.util
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -869,6 +871,25 @@ def calib_copy(b):
     b.rt.free(dst)
 
 
+def fresh_sections(keys):
+    """Each section in a process of its own (this script with --only), run before this process
+    touches the GPU: its buffers then land on fresh device memory, as the token's do. In one process,
+    after other sections had allocated and freed their copies, the same kernels ran up to 15 %
+    slower (the verify path at M = 2: 20.5 / 11.3 us alone, 21.9 / 12.4 with the token's 7.2 GB
+    resident, 23.0 / 13.9 after freeing them)."""
+    out = {}
+    for key in keys:
+        log(f"{key} ...")
+        p = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", key], stdout=subprocess.PIPE, text=True, timeout=600)
+        if p.returncode != 0:
+            raise SystemExit(f"bench.py: section {key} failed (exit {p.returncode})")
+        for line in p.stdout.splitlines():
+            if line.startswith("{"):
+                out.update(json.loads(line))
+        log(f"  {json.dumps(out.get(key))}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -900,32 +921,31 @@ def main():
         print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (every product runs on one MI355X; see DESIGN.md "
               "for how the rows would shard across GPUs)", file=sys.stderr)
         sys.exit(2)
-    q8rt = package()
-    b = Bench(q8rt)
-    name, cus = b.rt.device_info()
-    log(f"device: {name}, {cus} CUs")
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
                 ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers),
                 ("host_pointer_token_9b", host_pointer_token),
                 ("gguf_load_9b_layer", gguf_load), ("epilogues_9b", epilogues_9b))
     if a.only:
+        q8rt = package()
+        b = Bench(q8rt)
         want = a.only.split(",")
         for key, fn in sections:
             if key in want:
                 print(json.dumps({key: fn(b)}), flush=True)
         b.rt.close()
         return
+    extra = {}
+    if not a.no_extra:
+        extra = fresh_sections([key for key, _ in sections])
+    q8rt = package()
+    b = Bench(q8rt)
+    name, cus = b.rt.device_info()
+    log(f"device: {name}, {cus} CUs")
     if a.calib:
         calib_copy(b)
     seed0 = b.seed + 1
     per_token, ms_graph, ms_eager, kernels, roof, layers = decode_9b(b, a.steps, a.warmup)
     layer0 = {"seed0": seed0}
-    extra = {}
-    if not a.no_extra:
-        for key, fn in sections:
-            log(f"{key} ...")
-            extra[key] = fn(b)
-            log(f"  {json.dumps(extra[key])}")
     cpu = None
     if not a.no_cpu:
         log("CPU baseline ...")
