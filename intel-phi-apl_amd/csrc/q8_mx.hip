@@ -178,7 +178,7 @@ static int mx_choose(long rows, long cols)
 
 /* Whether the kernel takes t tokens of a product: a shape it runs (mx_choose), and only when
  * Q8_GEMV_MX sets the row groups. The VALU decode kernel, its lanes summed by q8_wave_sums, is
- * as fast or faster at every 9B shape measured at 3 and 4 tokens (4096x12288: 14.7 / 14.4 against
+ * as fast or faster at every 9B shape measured at 3 and 4 tokens (4096x12288: 13.4 / 14.5 against
  * 16.2 / 16.8 us; the pair 12288x4096: 24.4 / 25.3 against 27.2 / 28.5; 6144x4096: 8.6 / 9.0
  * against 12.0 / 11.6; 151936x4096: 141 / 163 against 141 / 169), and keeps each token's bits
  * those of its one-token product. */
