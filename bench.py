@@ -918,8 +918,8 @@ def main():
         summarize_verify(a.summarize_verify)
         return
     if a.gpus != 1:
-        print(f"bench.py: --gpus {a.gpus}: this build measures one GPU only (every product runs on one MI355X; see DESIGN.md "
-              "for how the rows would shard across GPUs)", file=sys.stderr)
+        print(f"bench.py: --gpus {a.gpus}: only one GPU is measured (every product runs on one MI355X; across GPUs the rows would "
+              "shard by whole 16-row groups, each GPU computing its slice of y)", file=sys.stderr)
         sys.exit(2)
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
                 ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers),
