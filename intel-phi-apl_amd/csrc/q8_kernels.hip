@@ -178,6 +178,9 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
 #pragma unroll
             for (int c = 0; c < 4; c++)
                 nv[s][c] = *(const float4 *)(e.nw + 16 * (u0 + 64 * s) + 4 * c);
+        /* keep them there: left to itself the scheduler issues them after the matrix, and the
+         * products of x and the norm weights, which every fma needs, then wait for all of it */
+        __builtin_amdgcn_sched_barrier(0);
     }
     uint4 q[RW][P][S];
     uint16_t dh[RW][P][S];
@@ -506,9 +509,8 @@ static bool gemv_epi_go(hipStream_t s, const void *w0, const void *w1, long rows
     const long kb = cols % 1024 ? 0 : cols / 1024;
     int rw, nw;
     gemv_choose(PAIR, 1, rows, kb, &rw, &nw); /* the fused-epilogue instances: as measured at one token */
-    /* the pair with the norm: its norm weights take 15 more registers (76), 6 waves a SIMD instead
-     * of 8, and 8 rows a workgroup (one round of fewer, longer workgroups) is the faster shape then
-     * (12288x4096: 20.7 against 21.3 us) */
+    /* the pair with the norm: its norm weights take more registers, and 8 rows a workgroup (one
+     * round of fewer, longer workgroups) is the faster shape then (12288x4096: 20.5 against 21.3 us) */
     if (PAIR && EPI == 1 && rw == 4 && rows % 8 == 0 && rows / 8 * nw >= 2048)
         rw = 8;
     if (!kb || rows % rw)
