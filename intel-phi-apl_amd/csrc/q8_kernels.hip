@@ -197,6 +197,10 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
                 dh[r][p][s] = wd[(u0 + 64 * s) >> 1];
             }
         }
+    /* every load issued before any arithmetic: left to itself the scheduler sinks the last rows'
+     * loads past the first rows' arithmetic, and past the wait for x, so they start a memory round
+     * trip late */
+    __builtin_amdgcn_sched_barrier(0);
 
     /* the norm: x <- nw * x at once, and per token the sum of x^2 (the lane's, then the wave's,
      * left in LDS for the final reduction, whose barrier covers it); s = 1 / sqrt(eps + sum / cols)
