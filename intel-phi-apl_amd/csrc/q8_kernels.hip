@@ -412,10 +412,10 @@ static bool gemv_go_rw(hipStream_t s, int nw, long kb, const uint8_t *a, const u
 /* The decode kernel's rows a workgroup (rw) and waves (nw) for a shape; kb = cols / 1024 */
 static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *nw_out)
 {
-    /* measured on the 9B shapes: 8 rows a workgroup (for the pair 4 at 1 and 3 tokens, the same
-     * 8 rows of loads a lane, and 8 at 2 and 4), one 1024-column step a wave, so K = 4096 takes 4
-     * waves and K = 12288 takes 12 */
-    int rw = pair ? (mt == 2 || mt == 4 ? 8 : 4) : 8, nw = (int)kb;
+    /* measured on the 9B shapes: 8 rows a workgroup (for the pair 4 at 1 token, the same 8 rows of
+     * loads a lane, and 8 at 2 to 4: 12288x4096 at 3 tokens 22.5 against 24.6 us), one 1024-column
+     * step a wave, so K = 4096 takes 4 waves and K = 12288 takes 12 */
+    int rw = pair ? (mt == 1 ? 4 : 8) : 8, nw = (int)kb;
     if (kb > 16 || kb == 3 || kb == 5 || kb == 7 || (kb > 8 && kb != 12 && kb != 16))
         nw = kb % 4 == 0 ? 4 : kb % 2 == 0 ? 2 : 1;
     /* 2 to 4 tokens at K = 12288: 16 rows, one 12-wave workgroup a CU and the grid in one round
