@@ -423,9 +423,10 @@ static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *
      * at 4) */
     if (!pair && mt >= 2 && nw == 12 && rows / 16 >= 256)
         rw = 16;
-    /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 2048 waves (two a
-     * SIMD) stream */
-    while (rw > 2 && rows / rw * nw < 2048)
+    /* small matrices (the 2B layer's): fewer rows a workgroup, so that at least 1024 waves (4096
+     * for the pair) stream. At one token 3072x2048 3.5 against 3.6 us at 4 rows (1536 waves) and 2,
+     * the pair 6144x2048 6.7 against 7.0 at 2 rows and 4, 2048x6144 4.8 against 4.9 at 8 and 4 */
+    while (rw > 2 && rows / rw * nw < (pair ? 4096 : 1024))
         rw /= 2;
     int erw, enw;
     if (gemv_env(&erw, &enw))
