@@ -200,15 +200,16 @@ def test_fast_gemm_prompt_shapes(rt, oracle, rows, cols):
         assert_parity(got, oracle.gemm_f64(q8, rows, cols, x), f"{rows}x{cols} t={t}")
 
 
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (6144, 2048)])
 @pytest.mark.parametrize("t", [1, 2, 3, 4])
-def test_fused_gate_up(rt, oracle, t):
-    """SiLU(G) * U for the 9B FFN pair (2 x 12288x4096), heavy-tailed scales."""
-    rows, cols = 12288, 4096
-    rng = np.random.default_rng(900 + t)
+def test_fused_gate_up(rt, oracle, rows, cols, t):
+    """SiLU(G) * U for the 9B and 2B FFN pairs (2 x 12288x4096, 2 x 6144x2048: 8, 4 and 2 rows a
+    workgroup), heavy-tailed scales."""
+    rng = np.random.default_rng(900 + t + rows)
     q8g = synth.q8_rows(rng, rows, cols, "lognormal")
     q8u = synth.q8_rows(rng, rows, cols, "lognormal")
     x = synth.x_f32(rng, t, cols)
-    say("swiglu", t)
+    say("swiglu", rows, cols, t)
     got = gpu_swiglu(rt, q8g, q8u, rows, cols, x)
     want = oracle.swiglu_f64(oracle.gemm_f64(q8g, rows, cols, x), oracle.gemm_f64(q8u, rows, cols, x))
     m = assert_parity(got, want, f"swiglu t={t}")
