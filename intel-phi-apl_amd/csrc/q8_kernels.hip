@@ -199,8 +199,11 @@ __device__ __forceinline__ void gemv_body(const uint8_t *__restrict__ w0, const 
         }
     /* every load issued before any arithmetic: left to itself the scheduler sinks the last rows'
      * loads past the first rows' arithmetic, and past the wait for x, so they start a memory round
-     * trip late */
-    __builtin_amdgcn_sched_barrier(0);
+     * trip late (4096x12288 at one token 10.85 against 11.0 us, at three 13.3 against 13.5). Not
+     * for 16 rows at two tokens, where the scheduler's own order measured faster (4096x12288: 11.4
+     * against 11.6 us) */
+    if constexpr (!(MT == 2 && RW == 16))
+        __builtin_amdgcn_sched_barrier(0);
 
     /* the norm: x <- nw * x at once, and per token the sum of x^2 (the lane's, then the wave's,
      * left in LDS for the final reduction, whose barrier covers it); s = 1 / sqrt(eps + sum / cols)
