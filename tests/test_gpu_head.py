@@ -8,7 +8,9 @@
   - the reference keeps gemm(t)[k] == gemv(x[k]) bit for bit (src/card/gemm.h:7). Here the
     reference-order kernel keeps it, the decode kernel (t <= 4) keeps it, and the matrix-core
     product (t >= 5, any K split) does not: its outputs differ from the one-token product's by the
-    F32 rounding of another summation order, bounded here by the parity bar.
+    F32 rounding of another summation order, bounded here by the parity bar;
+  - the reference's own gemm gate (scripts/check.sh:132-149) on its shapes and token counts, in the
+    reference-order kernel.
 """
 import ctypes as c
 import os
@@ -21,6 +23,9 @@ from parity import assert_parity, metrics
 pytestmark = pytest.mark.gpu
 
 VOCAB, HIDDEN, DRAFT = 151936, 4096, 32768
+# the token counts of the reference's gemm gate (scripts/check.sh:132-149), which crosses every
+# token chunk of its gemm (src/card/gemm.c)
+GATE_T = (1, 2, 3, 4, 5, 6, 7, 8, 9, 15, 16, 17, 40)
 
 
 def say(*a):
@@ -111,7 +116,7 @@ def test_draft_head_is_prefix(rt, oracle, head, t):
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (4096, 12288)])
 def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
     """gemm(t)[k] against gemv(x[k]) (src/card/gemm.h:7): bit for bit in the reference-order kernel at
-    every t and in the decode kernel at t = 2, 3, 4 (16 rows a workgroup at 2 and 4 tokens on
+    the token counts the reference's gate runs (GATE_T) and in the decode kernel at t = 2, 3, 4 (16 rows a workgroup at 2 and 4 tokens on
     4096x12288, 8 at 1 and 3: the rows a workgroup do not change a row's sums); at t >= 5 (the
     matrix-core product) and at every K split tried (1, 3 and the planner's), within the parity bar
     of the one-token product and of F64."""
@@ -119,13 +124,13 @@ def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
     try:
         X = np.random.default_rng(rows ^ cols).standard_normal((40, cols), dtype=np.float32)
         one = np.concatenate([h.product(X[k]) for k in range(40)])
-        one_exact = np.concatenate([h.product(X[k], exact=True) for k in range(8)])
+        one_exact = np.concatenate([h.product(X[k], exact=True) for k in range(40)])
         f64 = oracle.gemm_f64(h.q8, rows, cols, X)
         assert_parity(one, f64, "gemv per token")
         for t in (2, 3, 4):
             y = h.product(X[:t])
             assert np.array_equal(y.view(np.uint32), one[:t].view(np.uint32)), f"decode kernel t={t}"
-        for t in (3, 8):
+        for t in GATE_T:
             y = h.product(X[:t], exact=True)
             assert np.array_equal(y.view(np.uint32), one_exact[:t].view(np.uint32)), f"reference order t={t}"
         worst = 0.0
@@ -141,5 +146,27 @@ def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
             finally:
                 os.environ.pop("Q8_GEMM_KS", None)
         say(f"{rows}x{cols}: largest max-rel between gemm(t)[k] and gemv(x[k]) at t >= 3: {worst:.3e}")
+    finally:
+        h.close()
+
+
+@pytest.mark.parametrize("rows,cols,ts", [(1888, 512, GATE_T), (16, 512, (2, 8, 16)), (64, 512, (2, 8, 16)), (512, 512, (2, 8, 16))])
+def test_reference_gemm_gate(rt, oracle, rows, cols, ts):
+    """The reference's own gemm gate on its own shapes (scripts/check.sh:132-149: 1888x512 at every
+    token count of GATE_T, and 16, 64, 512 rows at 2, 8, 16 tokens): the reference-order kernel
+    keeps gemm(t)[k] == gemv(x[k]) bit for bit and equals the oracle's F32 order; the fast kernels
+    hold the parity bar against F64 at every t."""
+    h = Handle(rt, rows, cols, seed=7 * rows + cols)
+    try:
+        X = np.random.default_rng(rows + 17).standard_normal((max(ts), cols), dtype=np.float32)
+        one = np.concatenate([h.product(X[k], exact=True) for k in range(max(ts))])
+        f64 = oracle.gemm_f64(h.q8, rows, cols, X)
+        ref = oracle.gemm(h.q8, rows, cols, X)
+        assert np.array_equal(one.view(np.uint32), ref.view(np.uint32)), "one token at a time against the oracle's F32 order"
+        for t in ts:
+            say(f"gate {rows}x{cols} t={t}")
+            y = h.product(X[:t], exact=True)
+            assert np.array_equal(y.view(np.uint32), one[:t].view(np.uint32)), f"reference order t={t}"
+            assert_parity(h.product(X[:t]), f64[:t], f"fast t={t}")
     finally:
         h.close()
