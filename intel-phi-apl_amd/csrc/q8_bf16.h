@@ -25,7 +25,9 @@ __device__ __forceinline__ uint32_t pack_hi(float a, float b)
 __host__ __device__ constexpr int kcol(int kq) { return 8 * ((kq & 1) * 2 + (kq >> 1)); }
 
 /* 8 F32 values to their three bf16 limbs (8 each): hi = the top 16 bits, r = x - hi exactly,
- * mid = r's top 16 bits, lo = r - mid exactly (at most 8 significant bits) */
+ * mid = r's top 16 bits, lo = r - mid exactly (at most 8 significant bits). An infinite x is hi
+ * alone (x - hi would be NaN), so it reaches the sums as the infinity the F32 product sees; a NaN
+ * stays NaN in every limb's path. */
 __device__ __forceinline__ void xsplit8(float4 a, float4 c, uint4 &h, uint4 &m, uint4 &o)
 {
     const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
@@ -36,7 +38,7 @@ __device__ __forceinline__ void xsplit8(float4 a, float4 c, uint4 &h, uint4 &m, 
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             hi[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[j + e]) & 0xffff0000u);
-            const float r = v[j + e] - hi[e];
+            const float r = __builtin_isinf(v[j + e]) ? 0.0f : v[j + e] - hi[e];
             mid[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, r) & 0xffff0000u);
             lo[e] = r - mid[e];
         }

@@ -601,6 +601,38 @@ def test_permuting_row_groups_permutes_y(rt, rows, cols, t):
     assert np.array_equal(yp.view(np.uint32), y[:, rows_of].view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [2, 4, 16, 40])
+def test_non_finite_x_gives_the_references_classes(rt, oracle, t):
+    """An infinity or a NaN in x (token 0: +inf at one column, token 1: NaN at another, the last token
+    for t > 2: -inf at the last column) gives, output by output, the class the reference's F32 order
+    gives (oracle): NaN where the column's q or d is zero or x holds a NaN, an infinity with the sign
+    of q * d otherwise. The other tokens hold the parity bar; the reference-order kernel equals the
+    oracle bit for bit. Decode kernel (t <= 4), x-resident (16) and streaming (40) matrix cores,
+    whose three-limb split keeps an infinite x whole."""
+    rows, cols = 512, 4096
+    rng = np.random.default_rng(11 + t)
+    q8 = synth.q8_rows(rng, rows, cols)
+    x = synth.x_f32(rng, t, cols)
+    x[0, 77] = np.inf
+    x[1, 1000] = np.nan
+    bad = [0, 1]
+    if t > 2:
+        x[t - 1, cols - 1] = -np.inf
+        bad.append(t - 1)
+    say("non-finite x", t)
+    ref = oracle.gemm(q8, rows, cols, x)
+    got = gpu_gemm(rt, q8, rows, cols, x)
+    for k in bad:
+        assert not np.isfinite(ref[k]).any()
+        for cls in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(cls(got[k]), cls(ref[k])), f"token {k}: {cls.__name__}"
+    good = [k for k in range(t) if k not in bad]
+    if good:
+        assert_parity(got[good], oracle.gemm_f64(q8, rows, cols, x[good]), f"finite tokens t={t}")
+    ex = gpu_gemm(rt, q8, rows, cols, x, exact=True)
+    assert np.array_equal(ex, ref, equal_nan=True)
+
+
 def test_edge_scales(rt, oracle):
     """Zero scales give +0; subnormal, largest-finite and negative binary16 scales; q at -128..127 (the
     GGUF byte range, wider than the generator's)."""
