@@ -153,6 +153,15 @@ def decode_9b(b, steps, warmup):
     token()
     graph = b.lib.rt_graph_end(b.R)
     run = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(graph))  # noqa: E731
+    # settle, untimed, before the warmup steps: replays in groups of 10 for at least 150 ms, so that the
+    # timed steps start from the GPU's steady state whatever the warmup count (with 5 warmup steps and
+    # no settle, one run in two timed 20 steps 3.5 % slower: 1.470 against 1.420 ms a token)
+    t0, b.settle_replays = time.perf_counter(), 0
+    while time.perf_counter() - t0 < 0.15:
+        for _ in range(10):
+            run()
+        b.rt.sync()
+        b.settle_replays += 10
     for _ in range(warmup):
         run()
     ms_graph = b.timed(run, steps)
@@ -960,6 +969,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "settle_replays": b.settle_replays,
         "ms_per_step": round(ms_graph, 4),
         "higher_is_better": True,
         "scaling": "weak",
