@@ -27,28 +27,31 @@ __host__ __device__ constexpr int kcol(int kq) { return 8 * ((kq & 1) * 2 + (kq 
 /* 8 F32 values to their three bf16 limbs (8 each): hi = the top 16 bits, r = x - hi exactly,
  * mid = r's top 16 bits, lo = r - mid exactly (at most 8 significant bits). An infinite x is hi
  * alone (x - hi would be NaN), so it reaches the sums as the infinity the F32 product sees; a NaN
- * stays NaN in every limb's path. */
+ * stays NaN in every limb's path. The infinity test runs only when the largest |x| of the 8 is
+ * infinite (a few instructions for 8 values; the per-value test cost the streaming GEMM 2 us at
+ * M = 40 and 64). */
 __device__ __forceinline__ void xsplit8(float4 a, float4 c, uint4 &h, uint4 &m, uint4 &o)
 {
     const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-    uint32_t hh[4], mm[4], oo[4];
+    float hi[8], mid[8], lo[8];
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        float hi[2], mid[2], lo[2];
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            hi[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[j + e]) & 0xffff0000u);
-            const float r = __builtin_isinf(v[j + e]) ? 0.0f : v[j + e] - hi[e];
-            mid[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, r) & 0xffff0000u);
-            lo[e] = r - mid[e];
-        }
-        hh[j / 2] = pack_hi(hi[0], hi[1]);
-        mm[j / 2] = pack_hi(mid[0], mid[1]);
-        oo[j / 2] = pack_hi(lo[0], lo[1]);
+    for (int e = 0; e < 8; e++) {
+        hi[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[e]) & 0xffff0000u);
+        const float r = v[e] - hi[e];
+        mid[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, r) & 0xffff0000u);
+        lo[e] = r - mid[e];
     }
-    h = make_uint4(hh[0], hh[1], hh[2], hh[3]);
-    m = make_uint4(mm[0], mm[1], mm[2], mm[3]);
-    o = make_uint4(oo[0], oo[1], oo[2], oo[3]);
+    const float big = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                            fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
+    if (__builtin_expect(big == __builtin_inff(), 0)) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (__builtin_isinf(v[e]))
+                mid[e] = lo[e] = 0.0f;
+    }
+    h = make_uint4(pack_hi(hi[0], hi[1]), pack_hi(hi[2], hi[3]), pack_hi(hi[4], hi[5]), pack_hi(hi[6], hi[7]));
+    m = make_uint4(pack_hi(mid[0], mid[1]), pack_hi(mid[2], mid[3]), pack_hi(mid[4], mid[5]), pack_hi(mid[6], mid[7]));
+    o = make_uint4(pack_hi(lo[0], lo[1]), pack_hi(lo[2], lo[3]), pack_hi(lo[4], lo[5]), pack_hi(lo[6], lo[7]));
 }
 
 /* 8 int8 (two dwords) to 8 bf16 */
