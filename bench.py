@@ -130,7 +130,9 @@ def rotation(bench, rows, cols, copies_min=2, **kw):
     return [bench.matrix(rows, cols, **kw) for _ in range(n)]
 
 
-def decode_9b(b, steps, warmup):
+def token_9b(b):
+    """The 9B decode token's weights (distinct per layer) and activations, and the token as a function
+    that enqueues its 129 products; and its algorithmic bytes."""
     log(f"9B decode: {LAYERS} layers + head, {7230391808 / 1e9:.2f} GB of Q8_0 weights")
     layers = [dict(qkv=b.matrix(QKV, HIDDEN), out=b.matrix(HIDDEN, HIDDEN), gate=b.matrix(FFN, HIDDEN), up=b.matrix(FFN, HIDDEN),
                    down=b.matrix(HIDDEN, FFN)) for _ in range(LAYERS)]
@@ -148,6 +150,43 @@ def decode_9b(b, steps, warmup):
 
     per_token = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) +
                           alg_bytes(HIDDEN, FFN, 1)) + alg_bytes(VOCAB, HIDDEN, 1)
+    return layers, head, token, per_token
+
+
+TRACE_REPLAYS = 20
+
+
+def token_trace(b):
+    """The 9B token as one graph replayed TRACE_REPLAYS times, each replay alone on the GPU (the
+    stream idle before and after it), then launched eagerly as many times the same way, after one
+    untimed replay and one untimed eager token. Under rocprofv3 --kernel-trace every kernel of every
+    replay has its begin and end, so summarize_trace gives each of the 129 kernels of a replay its
+    duration and the gap from its end to the next kernel's begin. Also each replay's own time on the
+    stream's events, beside the trace's."""
+    layers, head, token, per_token = token_9b(b)
+    b.lib.rt_graph_begin(b.R)
+    token()
+    graph = b.lib.rt_graph_end(b.R)
+    run = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(graph))  # noqa: E731
+    out = {"replays": TRACE_REPLAYS, "products": 4 * LAYERS + 1, "bytes_per_token": per_token}
+    for key, fn in (("graph", run), ("eager", token)):
+        fn()
+        b.rt.sync()
+        ms = []
+        for _ in range(TRACE_REPLAYS):
+            ms.append(b.timed(fn, 1))
+        out[key] = {"ms_median": round(statistics.median(ms), 4), "ms_min": round(min(ms), 4)}
+        log(f"  {key}: {out[key]}")
+    b.lib.rt_graph_free(b.R, c.c_void_p(graph))
+    for L in layers:
+        for w in L.values():
+            b.rt.free(w)
+    b.rt.free(head)
+    return out
+
+
+def decode_9b(b, steps, warmup):
+    layers, head, token, per_token = token_9b(b)
     b.layers_9b, b.head_9b = layers, head  # the host-pointer token reuses them
     b.lib.rt_graph_begin(b.R)
     token()
@@ -416,7 +455,7 @@ def epilogues_9b(b):
     and the gate+up pair on RMS(x), the output and down products added to the residual stream,
     32 layers recorded as one graph, three ways: the products alone (4 launches a layer), with the
     epilogues fused into them (4), and with the norms and adds as kernels of their own (8,
-    Q8_EPI_APART=1). Weights rotate through 32 layers (7.2 GB), as in the token."""
+    rt_set_epi_apart). Weights rotate through 32 layers (7.2 GB), as in the token."""
     eps = 1e-6
     layers = [(b.matrix(QKV, HIDDEN), b.matrix(HIDDEN, HIDDEN), b.matrix(FFN, HIDDEN), b.matrix(FFN, HIDDEN), b.matrix(HIDDEN, FFN))
               for _ in range(LAYERS)]
@@ -440,8 +479,7 @@ def epilogues_9b(b):
     per = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) + alg_bytes(HIDDEN, FFN, 1))
     out = {"bytes_32_layers": per}
     for key, fn, apart in (("products_only", bare, False), ("epilogues_fused", with_epilogues, False), ("epilogues_apart", with_epilogues, True)):
-        if apart:
-            os.environ["Q8_EPI_APART"] = "1"
+        old = b.rt.set_epi_apart(apart)
         try:
             fn()
             b.rt.sync()
@@ -452,7 +490,7 @@ def epilogues_9b(b):
             ms = b.timed(lambda: L.rt_graph_launch(R, c.c_void_p(g)), 20)
             L.rt_graph_free(R, c.c_void_p(g))
         finally:
-            os.environ.pop("Q8_EPI_APART", None)
+            b.rt.set_epi_apart(old)
         out[key] = {"us_per_32_layers": round(1e3 * ms, 2), "GB/s": round(per / ms / 1e6, 1)}
     out["fused_saves_us_per_layer"] = round((out["epilogues_apart"]["us_per_32_layers"] - out["epilogues_fused"]["us_per_32_layers"]) / LAYERS, 3)
     for Lw in layers:
@@ -899,6 +937,92 @@ def fresh_sections(keys):
     return out
 
 
+TRACE_PROFILE = os.path.join(PROFILES, "token_trace_9b_m1.md")
+TRACE_PROFILE_CMDS = [
+    "rocprofv3 --kernel-trace --output-format csv -d gpurun_out/ttrace -o run -- python3 bench.py --only token_trace "
+    "> gpurun_out/ttrace.log 2>&1",
+    "python3 bench.py --summarize-trace gpurun_out",
+]
+
+
+def _replays(rows, n, last_grid):
+    """The trace's product kernels (rows: (name, grid, begin ns, end ns) in begin order) cut into
+    tokens: a token ends with the output head (the kernel of grid last_grid, its last product); runs
+    of any other length than n are dropped."""
+    runs, cur = [], []
+    for r in rows:
+        cur.append(r)
+        if r[1] == last_grid:
+            runs.append(cur)
+            cur = []
+    return [r for r in runs if len(r) == n]
+
+
+def summarize_trace(run_dir, out=TRACE_PROFILE):
+    """profiles/token_trace_9b_m1.md from the kernel trace of `bench.py --only token_trace`: the graph
+    replays and the eager tokens, each cut out of the trace by the idle stream around it; for the
+    replay of median span, every kernel's begin (from the replay's first begin), duration and gap to
+    the next kernel's begin; per product shape, the mean duration and gap over all replays."""
+    import csv
+    from collections import defaultdict
+
+    line = next(json.loads(l) for l in open(os.path.join(run_dir, "ttrace.log")) if l.startswith('{"token_trace"'))["token_trace"]
+    n = line["products"]
+    rows = []
+    for r in csv.DictReader(open(os.path.join(run_dir, "ttrace", "run_kernel_trace.csv"))):
+        k = _kname(r["Kernel_Name"])
+        if k.startswith(("gemv_", "gemm_")):
+            g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            rows.append((k, g, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    rows.sort(key=lambda r: r[2])
+    runs = _replays(rows, n, VOCAB // 8 * 256)
+    per = TRACE_REPLAYS + 1  # the untimed one first
+    if len(runs) != 2 * per:
+        raise SystemExit(f"summarize_trace: found {len(runs)} runs of {n} kernels, expected {2 * per}")
+    text = ["# The 9B decode token kernel by kernel: one graph replay in the kernel trace (rocprofv3)", "",
+            f"Workload: the 9B-class decode token at M = 1, {n} products ({LAYERS} x (QKV 6144x4096, out 4096x4096, gate+up 2x12288x4096 "
+            f"fused, down 4096x12288) + head 151936x4096), {line['bytes_per_token']} B a token, recorded once as a HIP graph. "
+            f"{TRACE_REPLAYS} replays, each alone on the stream (idle before and after), then {TRACE_REPLAYS} eager tokens the same way; "
+            "the first of each, untimed, is left out.", "",
+            "Commands (from the repository root):", "", "```"] + TRACE_PROFILE_CMDS + ["```", "",
+            f"Each replay's time on the stream's events in the same run (under the trace): graph median {line['graph']['ms_median']} ms "
+            f"(min {line['graph']['ms_min']}), eager median {line['eager']['ms_median']} ms (min {line['eager']['ms_min']}).", ""]
+
+    def table(mode, group):
+        spans = [(g[-1][3] - g[0][2]) / 1e3 for g in group]
+        busy = [sum((r[3] - r[2]) / 1e3 for r in g) for g in group]
+        gaps = [sum((g[i + 1][2] - g[i][3]) / 1e3 for i in range(len(g) - 1)) for g in group]
+        med = sorted(range(len(group)), key=lambda i: spans[i])[len(group) // 2]
+        text.extend([f"## {mode}", "",
+                     f"Over the {len(group)} {mode} runs: span (first begin to last end) median {statistics.median(spans):.1f} us "
+                     f"(min {min(spans):.1f}, max {max(spans):.1f}); kernels busy median {statistics.median(busy):.1f} us; gaps between "
+                     f"kernels median {statistics.median(gaps):.1f} us in all, {statistics.median(gaps) / (n - 1):.3f} us a boundary.", ""])
+        by = defaultdict(lambda: ([], []))
+        for g in group:
+            for i, r in enumerate(g):
+                by[(r[0], r[1])][0].append((r[3] - r[2]) / 1e3)
+                if i + 1 < len(g):
+                    by[(r[0], r[1])][1].append((g[i + 1][2] - r[3]) / 1e3)
+        text.extend(["Per kernel and grid, over every run:", "", "| Kernel | Grid (threads) | Launches | Mean duration us | Mean gap to the next us |",
+                     "|---|---|---|---|---|"])
+        for (k, gr), (d, gp) in sorted(by.items(), key=lambda kv: -sum(kv[1][0])):
+            text.append(f"| `{k}` | {gr} | {len(d)} | {statistics.fmean(d):.3f} | {statistics.fmean(gp) if gp else float('nan'):.3f} |")
+        g = group[med]
+        t0 = g[0][2]
+        text.extend(["", f"The {mode} run of median span ({spans[med]:.1f} us), kernel by kernel (us from its first begin):", "",
+                     "| # | Kernel | Grid | Begin | End | Duration | Gap to the next |", "|---|---|---|---|---|---|---|"])
+        for i, r in enumerate(g):
+            gap = f"{(g[i + 1][2] - r[3]) / 1e3:.3f}" if i + 1 < len(g) else ""
+            text.append(f"| {i} | `{r[0]}` | {r[1]} | {(r[2] - t0) / 1e3:.3f} | {(r[3] - t0) / 1e3:.3f} | {(r[3] - r[2]) / 1e3:.3f} | {gap} |")
+        text.append("")
+
+    table("graph", runs[1:per])
+    table("eager", runs[per + 1:])
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    open(out, "w").write("\n".join(text))
+    print(f"wrote {out}")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -914,6 +1038,8 @@ def main():
                     "profile commands) and exit")
     ap.add_argument("--summarize-gemm", metavar="DIR", help="write the GEMM rocprofv3 summary under profiles/ from DIR and exit")
     ap.add_argument("--summarize-verify", metavar="DIR", help="write the verify-path rocprofv3 summary under profiles/ from DIR and exit")
+    ap.add_argument("--summarize-trace", metavar="DIR", help="write the token-trace summary (a graph replay kernel by kernel) under "
+                    "profiles/ from DIR and exit")
     ap.add_argument("--calib", action="store_true", help="also copy 1 GiB three times with the plain copy kernel (the yardstick "
                     "for the HBM byte counters of a rocprofv3 --pmc run)")
     a = ap.parse_args()
@@ -926,6 +1052,9 @@ def main():
     if a.summarize_verify:
         summarize_verify(a.summarize_verify)
         return
+    if a.summarize_trace:
+        summarize_trace(a.summarize_trace)
+        return
     if a.gpus != 1:
         print(f"bench.py: --gpus {a.gpus}: only one GPU is measured (every product runs on one MI355X; across GPUs the rows would "
               "shard by whole 16-row groups, each GPU computing its slice of y)", file=sys.stderr)
@@ -935,6 +1064,7 @@ def main():
                 ("host_pointer_token_9b", host_pointer_token),
                 ("gguf_load_9b_layer", gguf_load), ("epilogues_9b", epilogues_9b))
     if a.only:
+        sections = sections + (("token_trace", token_trace),)
         q8rt = package()
         b = Bench(q8rt)
         want = a.only.split(",")

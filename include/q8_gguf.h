@@ -70,8 +70,11 @@ struct rt_gguf {
  * "path: reason" in err, the reason naming the byte where the header went wrong: the file cannot be
  * opened, does not start with "GGUF", ends inside the header, declares more keys or tensors than
  * its size could hold, uses a value type GGUF does not define, has a tensor of more than 4
- * dimensions or of an unknown ggml type, or an alignment of 0. general.alignment is taken from an
- * integer-typed key (32 when absent). The file is mapped, never read past the header. */
+ * dimensions or of an unknown ggml type, or an alignment of 0. general.alignment is read as the
+ * reference reads it, strtoull of the key's text whatever its type (32 when absent). Refused here
+ * where the reference's arithmetic would wrap 64 bits: a tensor whose offset + size overflows, an
+ * alignment or a data end that puts the data past 2^64 bytes. The file is mapped, never read past
+ * the header. */
 int rt_gguf_read(struct rt_gguf *g, const char *path, char *err, size_t err_cap);
 /* Frees the tables (gguf_free). Handles are not freed here: rt_gguf_release does that. */
 void rt_gguf_free(struct rt_gguf *g);

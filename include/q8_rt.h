@@ -30,7 +30,15 @@
  * reference's (src/card/rt.c:31-37, 274-285). The queue is a static of the library: not
  * reentrant, as the reference's is not (src/card/rt.c:216-226).
  *
- * Errors: every HIP call is checked; a failure prints the call and the HIP error and aborts. */
+ * Errors: every HIP call is checked; a failure prints the call and the HIP error and aborts.
+ *
+ * Waits: no call waits for the GPU without a deadline. A call that waits (for its y, a copy, the
+ * stream) and sees no completion within Q8_WAIT_S seconds (60 when unset) prints what it waited
+ * for and ends the process with _exit(3), as the reference's card does after about 60 s without
+ * its host (src/card/link.c:17-32).
+ *
+ * Environment: read once, by rt_init (Q8_DEVICE, Q8_EXACT, Q8_WAIT_S, Q8_UPLOAD_CHUNK,
+ * Q8_ABORT_EXIT), never on a product call; only Q8_EXACT changes a product's bits. */
 #ifndef Q8_RT_H
 #define Q8_RT_H
 
@@ -58,8 +66,10 @@ struct rt {
 /* ---- init (src/card/rt.h:38-39; rt.c:179-203) */
 
 /* Once, before any product: selects the GPU (Q8_DEVICE, default 0), creates the stream and
- * the staging buffers. threads is kept in R->threads and otherwise unused: the GPU grid
- * replaces the team. 0, or -1 when the GPU or its memory is not there. */
+ * the staging buffers, and reads the other settings from the environment (above). threads is
+ * kept in R->threads and otherwise unused: the GPU grid replaces the team. 0, or -1 when the GPU
+ * or its memory is not there. (Q8_ABORT_EXIT=n, 1..125: a caller's mistake ends the process with
+ * _exit(n) instead of abort(), for harnesses that check the message in a child process.) */
 int rt_init(struct rt *R, int threads);
 
 /* Releases the stream, the staging buffers and every uploaded matrix. An addition: the
@@ -105,7 +115,7 @@ void gemv_i_repack(const uint8_t *q8, long rows, long cols, void *out);
 const void *rt_q8_upload(struct rt *R, const uint8_t *q8, long rows, long cols);
 /* Addition (no reference counterpart; the GGUF loader's path): the same for GGUF Q8_0 rows read
  * from an open file at byte `offset`, straight into pinned staging in chunks of whole 16-row
- * groups (64 MiB, or Q8_UPLOAD_CHUNK bytes), each repacked on the device while the next is read.
+ * groups (64 MiB, or Q8_UPLOAD_CHUNK bytes, or rt_set_upload_chunk's), each repacked on the device while the next is read.
  * NULL when HBM is full or a read fails (errno set). */
 const void *rt_q8_upload_fd(struct rt *R, int fd, uint64_t offset, long rows, long cols);
 /* The same for a matrix already in form S in host memory (gemv_i_repack's output). */
@@ -136,9 +146,8 @@ void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float 
  * two runtimes) race. */
 void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* A round of n (1..RT_BATCH) products sharing x, none reading another's y: y[i] = X w[i]^T,
- * w[i] [rows[i] cols], as one launch where the kernel takes the shape (t <= 4; not while the
- * environment variable Q8_GEMV_MX sends 3 and 4 tokens to the matrix-core decode kernel, so that
- * each product's bits are its own launch's), else one after another. The device form of rt_gemv_q x n + rt_gemv_go, which
+ * w[i] [rows[i] cols], as one launch where the kernel takes the shape (t <= 4), else one after
+ * another; each y has the bits of its own single product. The device form of rt_gemv_q x n + rt_gemv_go, which
  * uses the same launch for queued decode products that share x (the DeltaNet quartet
  * QKV/GATE/BETA/ALPHA, src/apl/qwen35.apl:93-96). */
 void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
@@ -148,8 +157,7 @@ void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows,
 /* ---- the epilogues on either side of a product (additions; the reference computes them on its
  * host around the products: RMS = {⍺×⍵×(RMS_EPS+(+/⍵×⍵)÷≢⍵)*¯0.5}, src/apl/qwen35.apl:49, before a
  * layer's mixer and FFN, and the residual Z←X+… after them, qwen35.apl:131-139). Fused into the
- * decode kernel (t <= 4) for K = 2048, 4096, 6144 and 12288 (the residual into the matrix-core
- * decode kernel's store when Q8_GEMV_MX selects it at t = 3, 4) and the residual into the
+ * decode kernel (t <= 4) for K = 2048, 4096, 6144 and 12288 and the residual into the
  * matrix-core product's for t >= 5; other shapes run the norm or the add as a kernel of its own. The
  * norm is s = 1 / sqrt(eps + sum_k x[k]^2 / cols) per token in F32, xn[k] = nw[k] * (x[k] * s); its
  * sum runs in a fixed order for a given shape, so results repeat bit for bit, and a fused and a
@@ -176,7 +184,9 @@ void rt_q8_rows_dev(struct rt *R, const void *w, long cols, const long *rows, lo
  * fmaxf fold of a, as the host's rt_maxv then rt_index_of give it (src/card/rt.c:137-165) for
  * Next = {w index-of max/w} (src/apl/qwen35.apl:161). Deterministic. An addition. */
 void rt_argmax_dev(struct rt *R, const float *a, long n, long *idx);
-/* Device memory for activations, and copies to and from it on the runtime's stream. */
+/* Device memory for activations, and copies to and from it on the runtime's stream. rt_dev_free
+ * takes any HIP allocation of the device; every buffer that rt_q8_repack_dev registered inside it
+ * stops being a weight handle. */
 void *rt_dev_alloc(struct rt *R, long bytes);
 void rt_dev_free(struct rt *R, void *p);
 void rt_dev_upload(struct rt *R, void *dst, const void *src, long bytes);
@@ -215,8 +225,25 @@ void rt_prims_dev(struct rt *R, const int8_t *q, const float *x8, const float *c
 
 /* Product kernels: 0 = the fast kernels (default), 1 = the reference-order kernels, whose every
  * y is bit-identical to the reference's F32 host path (src/card/gemv.c:165-193 at one thread;
- * gemm.c:20-23 per token). Returns the previous mode. Q8_EXACT=1 in the environment sets 1. */
+ * gemm.c:20-23 per token). Returns the previous mode. Q8_EXACT=1 in the environment sets 1.
+ *
+ * In the fast kernels a token's y does not depend on how many tokens it was computed with, within
+ * t = 1..4 (the decode kernels) and within t >= 5 (the matrix-core product, whose K split is a
+ * function of the matrix's shape alone); across the two it differs within the parity bar. The
+ * reference-order kernels keep the reference's gemm(t)[k] == gemv(x[k]) (src/card/gemm.h:5-7) at
+ * every t. */
 int rt_set_exact(struct rt *R, int exact);
+
+/* Measurement and test settings (additions), each returning the previous value where it has one:
+ * rt_set_epi_apart(R, 1) runs every epilogue as a kernel of its own (the norm's sum then in that
+ * kernel's order: an ulp or so of its scale; the residual the same bits); rt_set_upload_chunk sets
+ * the upload's chunk in bytes (whole 16-row groups; the bits do not change); rt_gemm_force makes
+ * the matrix-core product use `ks` K splits (0: the planner's; other splits, other bits) and, with
+ * streaming != 0, the streaming kernel for one token tile instead of the x-resident one (the same
+ * sums). */
+int rt_set_epi_apart(struct rt *R, int apart);
+long rt_set_upload_chunk(struct rt *R, long bytes);
+void rt_gemm_force(struct rt *R, int streaming, int ks);
 
 /* Event timing on the runtime's stream: rt_timer_start, then rt_timer_stop returns the
  * milliseconds between them (waits for the stream). */
@@ -229,7 +256,7 @@ float rt_timer_stop(struct rt *R);
  * duration in microseconds, its name as rocprof prints it (64 bytes each in names, NUL-padded;
  * names may be NULL) and its grid in threads (grid may be NULL); reading clears the records.
  * rt_ktime(R, 1) also clears. */
-#define RT_K_GEMV 0      /* t <= 4, the decode kernels (VALU; at t = 3, 4 the matrix-core one where Q8_GEMV_MX selects it) */
+#define RT_K_GEMV 0      /* t <= 4, the decode kernels */
 #define RT_K_GEMV_PAIR 1 /* the fused gate/up pair, t <= 4 */
 #define RT_K_GEMM 2      /* t >= 5, the matrix-core kernel */
 #define RT_K_GEMM_PAIR 3

@@ -63,6 +63,9 @@ _SIGS = {
     "rt_argmax_dev": (None, [_vp, _vp, _long, _vp]),
     "rt_prims_dev": (None, [_vp, _vp, _vp, _vp, _vp, _long, _vp, _vp, _vp, _vp, _long]),
     "rt_set_exact": (_int, [_vp, _int]),
+    "rt_set_epi_apart": (_int, [_vp, _int]),
+    "rt_set_upload_chunk": (_long, [_vp, _long]),
+    "rt_gemm_force": (None, [_vp, _int, _int]),
     "rt_timer_start": (None, [_vp]),
     "rt_timer_stop": (_c.c_float, [_vp]),
     "rt_device_info": (None, [_vp, _c.c_char_p, _long, _c.POINTER(_int)]),
@@ -198,6 +201,17 @@ class Runtime:
 
     def set_exact(self, on):
         return self.lib.rt_set_exact(self.R, 1 if on else 0)
+
+    def set_epi_apart(self, on):
+        return self.lib.rt_set_epi_apart(self.R, 1 if on else 0)
+
+    def set_upload_chunk(self, nbytes):
+        return self.lib.rt_set_upload_chunk(self.R, int(nbytes))
+
+    def gemm_force(self, streaming=False, ks=0):
+        """The matrix-core product's kernel and K split for the following products (a test hook;
+        gemm_force() restores the planner's)."""
+        self.lib.rt_gemm_force(self.R, 1 if streaming else 0, int(ks))
 
     # ---- device memory
     def alloc(self, nbytes):

@@ -164,47 +164,6 @@ __device__ __forceinline__ void q8_wave_sums(float (&v)[V], int lane)
     }
 }
 
-/* v[c] of lane j of each quad (lanes 4b..4b+3) <- v[j] of lane c: a 4x4 transpose inside the quad,
- * in two exchanges (lanes j^1, then j^2). Each step is one v_cndmask_b32 whose first operand is
- * read through DPP from the partner lane: out = vcc ? keep : partner's value, with vcc the lanes
- * that keep (lanes whose bit 0, then bit 1, equals that of c). The two s_mov that set vcc come
- * first in every step, so a DPP read is at least two instructions after the VALU write of its
- * operand (the wait states gfx9 requires between them). The lane masks are the same in every
- * quad, so the step needs no lane index. */
-#define Q8_QT_STEP(out, keep, give, perm, mask)                                                                        \
-    asm volatile("s_mov_b32 vcc_lo, " mask "\n\ts_mov_b32 vcc_hi, " mask "\n\tv_cndmask_b32_dpp %0, %1, %2, vcc " perm   \
-                 " row_mask:0xf bank_mask:0xf"                                                                         \
-                 : "=v"(out)                                                                                           \
-                 : "v"(give), "v"(keep)                                                                                \
-                 : "vcc")
-__device__ __forceinline__ void q8_quad_transpose(uint32_t (&v)[4])
-{
-    uint32_t a[4];
-    /* c even keeps in lanes with j even (0x5555...), c odd in lanes with j odd (0xaaaa...) */
-    Q8_QT_STEP(a[0], v[0], v[1], "quad_perm:[1,0,3,2]", "0x55555555");
-    Q8_QT_STEP(a[2], v[2], v[3], "quad_perm:[1,0,3,2]", "0x55555555");
-    Q8_QT_STEP(a[1], v[1], v[0], "quad_perm:[1,0,3,2]", "0xaaaaaaaa");
-    Q8_QT_STEP(a[3], v[3], v[2], "quad_perm:[1,0,3,2]", "0xaaaaaaaa");
-    /* c < 2 keeps in lanes with j < 2 (0x3333...), c >= 2 in lanes with j >= 2 (0xcccc...) */
-    Q8_QT_STEP(v[0], a[0], a[2], "quad_perm:[2,3,0,1]", "0x33333333");
-    Q8_QT_STEP(v[1], a[1], a[3], "quad_perm:[2,3,0,1]", "0x33333333");
-    Q8_QT_STEP(v[2], a[2], a[0], "quad_perm:[2,3,0,1]", "0xcccccccc");
-    Q8_QT_STEP(v[3], a[3], a[1], "quad_perm:[2,3,0,1]", "0xcccccccc");
-}
-#undef Q8_QT_STEP
-
-/* the same for four 16-byte registers, component by component */
-__device__ __forceinline__ void q8_quad_transpose4(uint4 (&v)[4])
-{
-    uint32_t t[4];
-#define Q8_QT(f)                                                                                                       \
-    t[0] = v[0].f, t[1] = v[1].f, t[2] = v[2].f, t[3] = v[3].f;                                                        \
-    q8_quad_transpose(t);                                                                                              \
-    v[0].f = t[0], v[1].f = t[1], v[2].f = t[2], v[3].f = t[3];
-    Q8_QT(x) Q8_QT(y) Q8_QT(z) Q8_QT(w)
-#undef Q8_QT
-}
-
 /* SiLU(g) * u (src/apl/qwen35.apl:38; docs/model.md:29: Sig = 1 / (1 + exp(min(700, -g)))):
  * in binary32 exp(min(700, -g)) overflows to inf for -g > 88.7 exactly as exp(-g) does, so
  * the clamp changes nothing and is left out. */
@@ -249,13 +208,6 @@ extern long *q8_next_grid;
 
 /* Y = X W^T, t tokens, the fast kernels; W form S. w1 != NULL: the fused pair, Y = SiLU(X W0^T) * (X W1^T). */
 void q8_launch_gemv(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y);
-/* The same for t = 3 and 4 on the matrix cores (q8_mx.hip), res != NULL: Y = res + the product
- * (not with the pair; res may be y): true when launched, false when the kernel does not take the
- * shape (nothing launched). q8_gemv_mx_takes says which: the decode product, its fused residual
- * and the round all route on it, so that a product's bits do not depend on the entry point. */
-bool q8_launch_gemv_mx(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, float *y,
-                       const float *res = nullptr);
-bool q8_gemv_mx_takes(long rows, long cols, long t, bool pair);
 /* An epilogue on either side of a product (src/apl/qwen35.apl:49, 131-139). nw != NULL: the RMS
  * norm first, per token xn[k] = nw[k] * (x[k] * s) with s = 1 / sqrt(eps + sum_k x[k]^2 / cols);
  * res != NULL: Y = res + the product, res laid out as Y (it may be Y: the residual stream updated
@@ -289,12 +241,20 @@ int q8_launch_gemv_round_epi(q8_stream_t stream, int n, const void *const *w, co
                              float *const *y, q8_epi e);
 /* The reference's order, every y bit-identical to the reference's F32 host path. */
 void q8_launch_exact(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
-/* Y = X W^T for 5 <= t <= 64 on the matrix cores (and the sum of the K split's partials). part
- * holds q8_gemm_part_floats(rows, cols, t) floats, at most Q8_GEMM_PART_MAX. */
+/* Y = X W^T for 1 <= t <= 64 on the matrix cores (and the sum of the K split's partials); the
+ * runtime sends every product of t >= 5 tokens here, 64 tokens a launch. part holds
+ * q8_gemm_part_floats(rows, cols, t, o) floats, at most Q8_GEMM_PART_MAX. The K split is a
+ * function of (rows, cols) alone, so a token's output does not depend on t. o: test hooks, zero
+ * for the planner's choices (ks > 0: that many K splits; streaming: one token tile on the
+ * streaming kernel instead of the x-resident one, the same sums). */
 #define Q8_GEMM_PART_MAX (8L << 20)
+struct q8_gemm_opts {
+    int ks;
+    int streaming;
+};
 void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
-                         const float *res = nullptr);
-long q8_gemm_part_floats(long rows, long cols, long t);
+                         const float *res, q8_gemm_opts o);
+long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o);
 /* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
 void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
 /* z[i] = row rows[i] of w dequantised (q * d, exact), i < n; rows and z device arrays; an index

@@ -437,41 +437,29 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
 
 /* ---------------------------------------------------------------- launchers */
 
-/* The instantiated configurations: MG token tiles a workgroup (the product's MT token tiles in
- * groups of MG, over blockIdx.y), RT row tiles a wave, KP pairs a range, NW waves a workgroup.
- * x in LDS is MG * KP * 12 KiB (two ranges). */
+/* The instantiated configurations of gemm_mfma: MG token tiles a workgroup (the product's MT token
+ * tiles in groups of MG, over blockIdx.y), RT row tiles a wave, KP pairs a range, NW waves a
+ * workgroup. x in LDS is MG * KP * 12 KiB (two ranges). Measured on the 9B FFN matrices (12288 x
+ * 4096 and 4096 x 12288): 2-pair ranges and every token tile in one workgroup, so that the
+ * weights are read once; 8 waves at two token tiles, 16 at three and four. One token tile runs on
+ * gemm_xres (x resident); gemm_mfma<1, 1, 2, 16> computes the same sums and is kept for the tests
+ * that hold the two to the same bits. */
 struct gemm_cfg {
     int mg, rt, kp, nw;
 };
-#define GEMM_CFGS(X)                                                                                                   \
-    X(1, 1, 4, 8) X(1, 1, 2, 16) X(1, 1, 4, 16) X(1, 1, 8, 8) X(1, 1, 2, 8) X(2, 1, 4, 8) X(2, 1, 2, 8) X(2, 1, 2, 16) \
-        X(2, 1, 4, 16) X(3, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 8) X(4, 1, 2, 16) X(4, 1, 1, 16)
-#define GEMM_CFG_ROW(G, R, P, N) {G, R, P, N},
-static const gemm_cfg CFGS[] = {GEMM_CFGS(GEMM_CFG_ROW)};
-#undef GEMM_CFG_ROW
-#define NCFG ((int)(sizeof(CFGS) / sizeof(CFGS[0])))
-
-/* Q8_GEMM_CFG = "MG,RT,KP,NW" picks an instantiated configuration and Q8_GEMM_KS the K split,
- * for tuning sweeps. */
-static bool env_cfg(gemm_cfg *c)
-{
-    const char *v = getenv("Q8_GEMM_CFG");
-    int a = 0, b = 0, d = 0, e = 0;
-    if (!v || sscanf(v, "%d,%d,%d,%d", &a, &b, &d, &e) != 4)
-        return false;
-    for (int i = 0; i < NCFG; i++)
-        if (CFGS[i].mg == a && CFGS[i].rt == b && CFGS[i].kp == d && CFGS[i].nw == e) {
-            *c = CFGS[i];
-            return true;
-        }
-    return false;
-}
+#define GEMM_CFGS(X) X(1, 1, 2, 16) X(2, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 16)
 
 /* the x-resident kernel for one token tile: 2-pair ranges, 16 waves, segments of 8 ranges (x
  * limbs 96 KiB and scales 17 KiB of LDS: one workgroup a CU) */
 #define XRES_KP 2
 #define XRES_NW 16
 #define XRES_SC 8
+
+/* every configuration streams ranges of the same KP pairs, so a K split of cps ranges covers the
+ * same blocks in each: the split, and so the bits, do not depend on the kernel */
+#define GEMM_KP_CHECK(G, R, P, N) static_assert(P == XRES_KP, "every configuration ranges over XRES_KP pairs");
+GEMM_CFGS(GEMM_KP_CHECK)
+#undef GEMM_KP_CHECK
 
 /* workgroups of a kernel resident on the device at once (occupancy x compute units), asked of the
  * runtime once a kernel (n caches it) */
@@ -490,72 +478,47 @@ static long resident(K kernel, int threads, long &n)
     return n;
 }
 
-template <int MG, int RT, int KP, int NW>
-static long gemm_resident()
-{
-    static long n = 0;
-    return resident(gemm_mfma<MG, RT, KP, NW>, 64 * NW, n);
-}
-
-static long cfg_resident(const gemm_cfg &c, bool xres)
-{
-    static long nx = 0;
-    if (xres)
-        return resident(gemm_xres<XRES_KP, XRES_NW, XRES_SC>, 64 * XRES_NW, nx);
-#define GEMM_RES(G, R, P, N)                                                                                           \
-    if (c.mg == G && c.rt == R && c.kp == P && c.nw == N)                                                              \
-        return gemm_resident<G, R, P, N>();
-    GEMM_CFGS(GEMM_RES)
-#undef GEMM_RES
-    fprintf(stderr, "q8_gemm: no kernel for MG %d RT %d KP %d NW %d\n", c.mg, c.rt, c.kp, c.nw);
-    abort();
-}
-
 /* a product's kernel and K split */
 struct gemm_plan {
     gemm_cfg c;
-    bool xres; /* gemm_xres (one token tile, c = 1, 1, XRES_KP, XRES_NW) rather than gemm_mfma<c> */
+    bool xres; /* gemm_xres (one token tile) rather than gemm_mfma<c> */
     int ks, cps;
 };
 
-static gemm_plan plan_of(long rows, long cols, long t)
+/* The K split of a rows x cols matrix: ks splits of cps ranges of XRES_KP block pairs (the last may
+ * hold fewer), a function of the shape alone, so that a token's output has the same bits whatever
+ * the number of tokens it is computed with (5 to 64 a launch, and every 64-token launch of a longer
+ * X). As many splits as fill the device with one resident round of the x-resident kernel's
+ * workgroups (256 rows each), fewer if the partials of a 64-token launch would not fit the
+ * workspace. ks_force > 0 sets the split count instead (a test hook: other splits, other bits). */
+static void split_of(long rows, long cols, int ks_force, int *ks, int *cps)
 {
-    const long mt = (t + 15) / 16;
-    /* measured on the 9B FFN matrices (12288 x 4096 and 4096 x 12288): 16 waves and 2-pair
-     * ranges, every token tile in one workgroup, so the weights are read once; one token tile
-     * keeps x resident */
-    const gemm_cfg def = mt == 1 ? gemm_cfg{1, 1, XRES_KP, XRES_NW} : mt == 2 ? CFGS[7] : mt == 3 ? CFGS[10] : CFGS[12];
-    gemm_plan p = {def, mt == 1, 0, 0};
-    gemm_cfg e;
-    if (env_cfg(&e) && e.mg <= mt)
-        p.c = e, p.xres = false;
-    /* a wave owns RT row tiles: RT must divide the matrix's row tiles (the defaults have RT = 1) */
-    if ((rows / 16) % p.c.rt)
-        p.c = def, p.xres = mt == 1;
-    const gemm_cfg &c = p.c;
-    const long tiles = (rows + 16L * c.nw * c.rt - 1) / (16L * c.nw * c.rt);
+    static long nx = 0;
+    const long tiles = (rows + 16L * XRES_NW - 1) / (16L * XRES_NW);
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
-    const long groups = (mt + c.mg - 1) / c.mg;
-    const long ranges = (np + c.kp - 1) / c.kp;
-    /* the K split: as many splits as fill the device with one resident round of workgroups, each
-     * streaming cps ranges; fewer if the partials would not fit the workspace */
-    long split = cfg_resident(c, p.xres) / (tiles * groups);
-    const char *v = getenv("Q8_GEMM_KS");
-    if (v && atol(v) > 0)
-        split = atol(v);
+    const long ranges = (np + XRES_KP - 1) / XRES_KP;
+    long split = ks_force > 0 ? ks_force : resident(gemm_xres<XRES_KP, XRES_NW, XRES_SC>, 64 * XRES_NW, nx) / tiles;
     split = split < 1 ? 1 : split > ranges ? ranges : split;
     long per = (ranges + split - 1) / split;
-    while (per < ranges && (ranges + per - 1) / per * mt * 16 * rows > Q8_GEMM_PART_MAX)
+    while (per < ranges && (ranges + per - 1) / per * 64 * rows > Q8_GEMM_PART_MAX)
         per++;
-    p.cps = (int)per;
-    p.ks = (int)((ranges + per - 1) / per);
+    *cps = (int)per;
+    *ks = (int)((ranges + per - 1) / per);
+}
+
+static gemm_plan plan_of(long rows, long cols, long t, q8_gemm_opts o)
+{
+    const long mt = ((t < 64 ? t : 64) + 15) / 16;
+    static const gemm_cfg CFG[5] = {{0, 0, 0, 0}, {1, 1, 2, 16}, {2, 1, 2, 8}, {3, 1, 2, 16}, {4, 1, 2, 16}};
+    gemm_plan p = {CFG[mt], mt == 1 && !o.streaming, 0, 0};
+    split_of(rows, cols, o.ks, &p.ks, &p.cps);
     return p;
 }
 
-long q8_gemm_part_floats(long rows, long cols, long t)
+long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o)
 {
-    const gemm_plan p = plan_of(rows, cols, t);
-    return p.ks > 1 ? (long)p.ks * ((t + 15) / 16) * 16 * rows : 0;
+    const gemm_plan p = plan_of(rows, cols, t, o);
+    return p.ks > 1 ? (long)p.ks * (((t < 64 ? t : 64) + 15) / 16) * 16 * rows : 0;
 }
 
 template <int MG, int RT, int KP, int NW>
@@ -569,10 +532,10 @@ static void gemm_go(hipStream_t s, const void *w, long rows, long cols, const fl
 }
 
 void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
-                         const float *res)
+                         const float *res, q8_gemm_opts o)
 {
     hipStream_t s = (hipStream_t)stream;
-    const gemm_plan p = plan_of(rows, cols, t);
+    const gemm_plan p = plan_of(rows, cols, t, o);
     const int ks = p.ks, cps = p.cps;
     float *out = ks > 1 ? part : y;
     const float *r1 = ks > 1 ? nullptr : res;

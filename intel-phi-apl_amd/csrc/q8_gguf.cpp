@@ -308,18 +308,25 @@ bool parse(struct rt_gguf *g, const uint8_t *base, uint64_t size, char *why, siz
             return false;
         }
     }
+    /* general.alignment as the reference reads it: strtoull of the key's text, whatever its type
+     * (gguf_reader.c:198-202), so a string "64" or an f32 64 give 64 */
     uint64_t alignment = 32;
     for (uint64_t i = 0; i < g->n_keys && c.ok(); i++) {
         bool integer = false;
         uint64_t num = 0;
-        if (parse_key(c, g->keys[i], &integer, &num) && integer && strcmp(g->keys[i].name, "general.alignment") == 0)
-            alignment = num;
+        if (parse_key(c, g->keys[i], &integer, &num) && strcmp(g->keys[i].name, "general.alignment") == 0)
+            alignment = strtoull(g->keys[i].text, nullptr, 10);
     }
     uint64_t data_end = 0;
     for (uint64_t i = 0; i < g->n_tensors && c.ok(); i++) {
         struct rt_gguf_tensor &t = g->tensors[i];
         if (!parse_tensor(c, t))
             break;
+        /* an offset and size whose end wraps 64 bits would pass every later size check */
+        if (t.bytes > UINT64_MAX - t.offset) {
+            snprintf(why, why_cap, "tensor %s: offset %" PRIu64 " + %" PRIu64 " bytes overflows 64 bits", t.name, t.offset, t.bytes);
+            return false;
+        }
         g->data_bytes += t.bytes;
         data_end = t.offset + t.bytes > data_end ? t.offset + t.bytes : data_end;
     }
@@ -332,7 +339,17 @@ bool parse(struct rt_gguf *g, const uint8_t *base, uint64_t size, char *why, siz
         return false;
     }
     g->header_end = c.offset();
+    /* the reference's arithmetic wraps for an alignment near 2^64 (a negative key, for example);
+     * such a file is refused here */
+    if (alignment - 1 > UINT64_MAX - g->header_end) {
+        snprintf(why, why_cap, "general.alignment %" PRIu64 " puts the data past 2^64 bytes", alignment);
+        return false;
+    }
     g->data_start = (g->header_end + alignment - 1) / alignment * alignment;
+    if (data_end > UINT64_MAX - g->data_start) {
+        snprintf(why, why_cap, "the tensors end past 2^64 bytes (data at %" PRIu64 ", their end %" PRIu64 " past it)", g->data_start, data_end);
+        return false;
+    }
     g->need = g->data_start + data_end;
     for (uint64_t i = 0; i < g->n_tensors; i++)
         g->tensors[i].offset += g->data_start;

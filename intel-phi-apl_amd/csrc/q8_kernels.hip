@@ -379,18 +379,6 @@ __global__ __launch_bounds__(64 * NW) void gemv_round_norm(q8_round r, long cols
     gemv_body<MT, RW, S, NW, 0, 1>((const uint8_t *)r.w[p], nullptr, r.rows[p], cols, x, x_stride, r.y[p], ((long)blockIdx.x - r.start[p]) * RW, e);
 }
 
-/* Q8_GEMV_CFG = "RW,NW" overrides the decode kernel's rows and waves a workgroup, for tuning sweeps. */
-static bool gemv_env(int *rw, int *nw)
-{
-    static int cached = -1, crw = 0, cnw = 0;
-    if (cached < 0) {
-        const char *v = getenv("Q8_GEMV_CFG");
-        cached = v && sscanf(v, "%d,%d", &crw, &cnw) == 2 ? 1 : 0;
-    }
-    *rw = crw, *nw = cnw;
-    return cached == 1;
-}
-
 template <int MT, int RW, int S, int NW, int PAIR>
 static void gemv_launch(hipStream_t s, const uint8_t *a, const uint8_t *b, long rows, long cols, const float *x, long xs, float *y)
 {
@@ -431,9 +419,6 @@ static void gemv_choose(int pair, int mt, long rows, long kb, int *rw_out, int *
      * the pair 6144x2048 6.7 against 7.0 at 2 rows and 4, 2048x6144 4.8 against 4.9 at 8 and 4 */
     while (rw > 2 && rows / rw * nw < (pair ? 4096 : 1024))
         rw /= 2;
-    int erw, enw;
-    if (gemv_env(&erw, &enw))
-        rw = erw, nw = enw;
     *rw_out = rw, *nw_out = nw;
 }
 
@@ -442,8 +427,6 @@ static void gemv_go(hipStream_t s, const void *w0, const void *w1, long rows, lo
 {
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
     const long kb = cols % 1024 ? 0 : cols / 1024;
-    if (MT >= 3 && q8_launch_gemv_mx(s, a, b, rows, cols, x, xs, MT, y))
-        return;
     int rw, nw;
     gemv_choose(PAIR, MT, rows, kb, &rw, &nw);
     if (kb && rows % rw == 0) {
@@ -544,10 +527,6 @@ int q8_launch_gemv_epi(q8_stream_t stream, const void *w0, const void *w1, long 
 {
     if (t < 1 || t > 4 || (e.nw != nullptr) == (e.res != nullptr) || (w1 && e.res))
         return -1;
-    /* the residual of a product the matrix-core decode kernel takes: added in its store, so that
-     * the bits are that product's plus one F32 add */
-    if (e.res && q8_gemv_mx_takes(rows, cols, t, false))
-        return q8_launch_gemv_mx(stream, w0, w1, rows, cols, x, x_stride, t, y, e.res) ? 0 : -1;
     hipStream_t s = (hipStream_t)stream;
     bool done;
     switch (t) {
@@ -684,11 +663,6 @@ int q8_launch_gemv_round(q8_stream_t stream, int n, const void *const *w, const 
     long kb;
     if (!round_plan(n, w, rows, cols, t, y, r, nw, kb))
         return -1;
-    /* a product the matrix-core decode kernel takes runs as its own launch, so that its bits are
-     * the single product's */
-    for (int i = 0; i < n; i++)
-        if (q8_gemv_mx_takes(rows[i], cols, t, false))
-            return -1;
     constexpr int RW = ROUND_RW;
     hipStream_t s = (hipStream_t)stream;
     bool done = false;

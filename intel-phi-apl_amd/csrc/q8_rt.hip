@@ -20,6 +20,7 @@
 
 #include "../../include/q8_rt.h"
 #include "q8_device.h"
+#include "q8_wait.h"
 
 #define HIPCHECK(call)                                                                                                 \
     do {                                                                                                               \
@@ -30,20 +31,21 @@
         }                                                                                                              \
     } while (0)
 
+/* Q8_ABORT_EXIT=n (1..125), read by rt_init: a caller's mistake ends the process with _exit(n)
+ * instead of abort(), for test harnesses that check the message of an expected failure in a child
+ * process without a SIGABRT. */
+static int abort_exit = 0;
+
 /* A caller's mistake (a bad shape, an unregistered handle, a misaligned address): the reason on
- * stderr, then abort(), as the reference's entry points fail, before anything is launched.
- * Q8_ABORT_EXIT=n (1..125) ends the process with _exit(n) instead, for test harnesses that check
- * the message of an expected failure in a child process without a SIGABRT. */
+ * stderr, then abort(), as the reference's entry points fail, before anything is launched. */
 [[noreturn]] static void failv(const char *fn, const char *fmt, va_list ap)
 {
     fprintf(stderr, "q8_rt: %s: ", fn);
     vfprintf(stderr, fmt, ap);
     fputc('\n', stderr);
     fflush(stderr);
-    const char *v = getenv("Q8_ABORT_EXIT");
-    const int code = v ? atoi(v) : 0;
-    if (code >= 1 && code <= 125)
-        _exit(code);
+    if (abort_exit >= 1 && abort_exit <= 125)
+        _exit(abort_exit);
     abort();
 }
 
@@ -89,7 +91,13 @@ struct ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    int exact = 0;
+    /* the settings, from the environment at rt_init or from their setters; nothing reads the
+     * environment on a product call */
+    int exact = 0;          /* Q8_EXACT, rt_set_exact */
+    int epi_apart = 0;      /* rt_set_epi_apart */
+    double wait_s = Q8_WAIT_DEFAULT_S; /* Q8_WAIT_S: every host wait's deadline */
+    size_t upload_chunk = (size_t)64 << 20; /* Q8_UPLOAD_CHUNK, rt_set_upload_chunk */
+    q8_gemm_opts gemm_opts = {0, 0};        /* rt_gemm_force */
     /* staging for the host-pointer products, in floats: pinned x and y, x's copy in HBM */
     float *hx = nullptr, *hy = nullptr, *dx = nullptr;
     size_t x_cap = 0, y_cap = 0;
@@ -128,7 +136,9 @@ struct ctx {
 
 constexpr size_t KT_MAX = 16384;
 
-/* The runtime rt_init set up last: rt_q8_row takes no struct rt (src/card/rt.h:85) and uses it. */
+/* The runtimes alive, in the order rt_init set them up; rt_q8_row takes no struct rt
+ * (src/card/rt.h:85) and uses the last of them. */
+std::vector<ctx *> live;
 ctx *current = nullptr;
 
 ctx *get(struct rt *R, const char *fn)
@@ -160,6 +170,40 @@ void check_dev_ptr(const char *fn, const void *p, const char *what)
 {
     if (!p || ((uintptr_t)p & 15))
         failf(fn, "%s must be a 16-byte aligned device address", what);
+}
+
+/* Waits, each bounded by the runtime's deadline (q8_wait_until): the stream idle, an event done.
+ * A HIP error seen while polling (a kernel that failed) stops the process with the call's name. */
+void sync_stream(ctx *c, const char *what)
+{
+    q8_wait_until(
+        [&] {
+            const hipError_t e = hipStreamQuery(c->stream);
+            if (e == hipErrorNotReady)
+                return false;
+            if (e != hipSuccess) {
+                fprintf(stderr, "q8_rt: %s: the stream reports %s\n", what, hipGetErrorString(e));
+                abort();
+            }
+            return true;
+        },
+        c->wait_s, what);
+}
+
+void sync_event(ctx *c, hipEvent_t ev, const char *what)
+{
+    q8_wait_until(
+        [&] {
+            const hipError_t e = hipEventQuery(ev);
+            if (e == hipErrorNotReady)
+                return false;
+            if (e != hipSuccess) {
+                fprintf(stderr, "q8_rt: %s: the event reports %s\n", what, hipGetErrorString(e));
+                abort();
+            }
+            return true;
+        },
+        c->wait_s, what);
 }
 
 /* *p = a pinned host buffer of n floats (the old one freed: no call is in flight when it grows) */
@@ -223,55 +267,38 @@ float *reserve_epi(ctx *c, size_t n)
 
 void reserve_gemm(ctx *c, long rows, long cols, long t)
 {
-    if (!c->part && q8_gemm_part_floats(rows, cols, t) > 0) {
+    if (!c->part && q8_gemm_part_floats(rows, cols, t, c->gemm_opts) > 0) {
         no_capture(c, "the matrix-core product's partial sums");
         HIPCHECK(hipMalloc((void **)&c->part, (size_t)Q8_GEMM_PART_MAX * sizeof(float)));
     }
-    if (q8_gemm_part_floats(rows, cols, t) > Q8_GEMM_PART_MAX)
+    if (q8_gemm_part_floats(rows, cols, t, c->gemm_opts) > Q8_GEMM_PART_MAX)
         fail("the matrix-core product", "its K-split partials exceed the workspace (a planning error)");
 }
 
-/* Whether t tokens of a product go to the matrix-core product (else the decode kernels, which take
- * at most 4): from 5 tokens on. Q8_MFMA_MIN_T = n (1..5) moves the threshold down, for measuring
- * the two on the same shapes (the matrix-core decode kernel at 3 and 4 tokens is faster than the
- * product at the 9B shapes, so the threshold stays). */
-bool on_matrix_cores(long t)
-{
-    static long min_t = -1;
-    if (min_t < 0) {
-        const char *v = getenv("Q8_MFMA_MIN_T");
-        min_t = v && atol(v) >= 1 && atol(v) <= 5 ? atol(v) : 5;
-    }
-    return t >= min_t;
-}
+/* Whether a product of t tokens runs on the matrix cores (every 64-token launch of it, the last
+ * one too, however few tokens it holds, so that a token's bits do not depend on t), else on the
+ * decode kernels, which take at most 4 tokens a launch. */
+bool on_matrix_cores(long t) { return t >= 5; }
 
-/* Y = X W^T for t >= 5 tokens, 64 at a time; res != NULL: Y = res + X W^T (res may be Y), added in
- * the matrix-core product's store or partial sum. part != NULL: the K-split partials go there (at
- * most Q8_GEMM_PART_MAX floats) instead of the runtime's workspace, and nothing is allocated. */
+/* Y = X W^T for t >= 5 tokens on the matrix cores, 64 at a time; res != NULL: Y = res + X W^T (res
+ * may be Y), added in the matrix-core product's store or partial sum. part != NULL: the K-split
+ * partials go there (at most Q8_GEMM_PART_MAX floats) instead of the runtime's workspace, and
+ * nothing is allocated. */
 void gemm_tokens(ctx *c, const void *w, long rows, long cols, const float *x, long xs, long t, float *y, const float *res = nullptr,
                  float *part = nullptr)
 {
     const q8_stream_t s = (q8_stream_t)c->stream;
     for (long k = 0; k < t; k += 64) {
         const long n = t - k < 64 ? t - k : 64;
-        if (!on_matrix_cores(n)) {
-            if (!res) {
-                q8_launch_gemv(s, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows);
-            } else if (q8_launch_gemv_epi(s, w, nullptr, rows, cols, x + k * xs, xs, n, y + k * rows, q8_epi{nullptr, 0.0f, res + k * rows}) != 0) {
-                float *tmp = reserve_epi(c, (size_t)(n * rows));
-                q8_launch_gemv(s, w, nullptr, rows, cols, x + k * xs, xs, n, tmp);
-                q8_launch_add(s, res + k * rows, tmp, n * rows, y + k * rows);
-            }
-            continue;
-        }
         if (part) {
-            if (q8_gemm_part_floats(rows, cols, n) > Q8_GEMM_PART_MAX)
+            if (q8_gemm_part_floats(rows, cols, n, c->gemm_opts) > Q8_GEMM_PART_MAX)
                 failf("rt_gemm_dev_noalloc", "the K-split partials of %ld x %ld at %ld tokens exceed the %ld-float scratch", rows, cols, n,
                       (long)Q8_GEMM_PART_MAX);
         } else {
             reserve_gemm(c, rows, cols, n);
         }
-        q8_launch_gemm_mfma(s, w, rows, cols, x + k * xs, xs, n, y + k * rows, part ? part : c->part, res ? res + k * rows : nullptr);
+        q8_launch_gemm_mfma(s, w, rows, cols, x + k * xs, xs, n, y + k * rows, part ? part : c->part, res ? res + k * rows : nullptr,
+                            c->gemm_opts);
     }
 }
 
@@ -337,14 +364,6 @@ void kt_cancel(ctx *c)
     c->kt.pop_back();
 }
 
-/* Q8_EPI_APART=1 runs every epilogue as a kernel of its own (the same results: the norm's sum in
- * its separate kernel's order, the residual the same bits), for comparisons of the two. */
-bool epi_apart()
-{
-    const char *v = getenv("Q8_EPI_APART");
-    return v && v[0] == '1';
-}
-
 /* Y = X W^T (or the fused pair) with an epilogue: the RMS norm of x first (e.nw) or the residual
  * added to Y (e.res). Fused into the decode kernel where it takes the shape; else the norm apart
  * into the workspace and then the product, or the residual in the matrix-core product's store, or
@@ -352,7 +371,7 @@ bool epi_apart()
 void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, const float *x, long xs, long t, float *y, q8_epi e)
 {
     const q8_stream_t s = (q8_stream_t)c->stream;
-    const bool apart = epi_apart();
+    const bool apart = c->epi_apart != 0;
     if (!c->exact && t <= 4 && !apart) {
         const bool timed = kt_begin(c, RT_K_GEMV + (w1 ? 1 : 0), rows, cols, t);
         if (q8_launch_gemv_epi(s, w0, w1, rows, cols, x, xs, t, y, e) == 0) {
@@ -369,7 +388,7 @@ void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, c
         product(c, w0, w1, rows, cols, xn, cols, t, y);
         return;
     }
-    if (!c->exact && !w1 && !apart) {
+    if (!c->exact && !w1 && !apart && on_matrix_cores(t)) {
         kt_begin(c, RT_K_GEMM, rows, cols, t);
         gemm_tokens(c, w0, rows, cols, x, xs, t, y, e.res);
         launched("the product and its residual");
@@ -409,25 +428,33 @@ bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long co
  * visible to the host: a one-lane kernel queued last sets the pinned flag to this call's number
  * and the host polls it. Each kernel's end writes back its stores, and the flag's release store
  * follows them, so y in pinned memory is complete when the flag reads the number. This is 4.4 us a
- * call quicker than hipStreamSynchronize (18.4 against 14.0 us for a 4096x4096 rt_gemv). After
- * two seconds of polling it waits on the stream instead, which also reports a kernel that failed. */
-void wait_done(ctx *c)
+ * call quicker than hipStreamSynchronize (18.4 against 14.0 us for a 4096x4096 rt_gemv). Every
+ * 64th poll past the first 4096 also asks the stream, which reports a kernel that failed; the
+ * wait ends at the runtime's deadline (q8_wait_until). */
+void wait_done(ctx *c, const char *what)
 {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     HIPCHECK(hipStreamIsCapturing(c->stream, &st));
     if (st != hipStreamCaptureStatusNone)
-        fail("a host-pointer product", "it waits for its result, so it cannot be recorded into a graph (use the _dev entry points)");
+        fail(what, "it waits for its result, so it cannot be recorded into a graph (use the _dev entry points)");
     const unsigned seq = ++c->flag_seq;
     q8_launch_flag((q8_stream_t)c->stream, c->flag, seq);
     launched("the completion flag");
-    const auto t0 = std::chrono::steady_clock::now();
-    for (long spins = 0; __atomic_load_n(c->flag, __ATOMIC_ACQUIRE) != seq; spins++) {
-        __builtin_ia32_pause();
-        if ((spins & 1023) == 1023 && std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
-            HIPCHECK(hipStreamSynchronize(c->stream));
-            return;
-        }
-    }
+    unsigned long polls = 0;
+    q8_wait_until(
+        [&] {
+            if (__atomic_load_n(c->flag, __ATOMIC_ACQUIRE) == seq)
+                return true;
+            if (++polls > 4096 && (polls & 63) == 0) {
+                const hipError_t e = hipStreamQuery(c->stream);
+                if (e != hipSuccess && e != hipErrorNotReady) {
+                    fprintf(stderr, "q8_rt: %s: the stream reports %s\n", what, hipGetErrorString(e));
+                    abort();
+                }
+            }
+            return false;
+        },
+        c->wait_s, what);
 }
 
 /* A round over host pointers: distinct x staged once, every product (those sharing x as one
@@ -436,7 +463,7 @@ void wait_done(ctx *c)
  * into pinned host memory, which the host reads after the wait. Asynchronous copies in both
  * directions cost more: 19.2 / 32.9 / 148.7 us against 17.6 / 24.3 / 126.6 us a call for the
  * 4096x4096, 12288x4096 and 151936x4096 GEMVs, 152 against 25 us at 4096x4096 with 4 tokens. */
-void run_round(ctx *c, job *jobs, int n)
+void run_round(ctx *c, job *jobs, int n, const char *what)
 {
     size_t nx = 0, ny = 0;
     for (int i = 0; i < n; i++) {
@@ -489,7 +516,7 @@ void run_round(ctx *c, job *jobs, int n)
         if (!done[i])
             product(c, j.w, nullptr, j.rows, j.cols, c->dx + j.x_off, j.cols, j.t, c->hy + j.y_off);
     }
-    wait_done(c);
+    wait_done(c, what);
     for (int i = 0; i < n; i++)
         memcpy(jobs[i].y, c->hy + jobs[i].y_off, sizeof(float) * (size_t)(jobs[i].t * jobs[i].rows));
 }
@@ -528,13 +555,23 @@ int rt_init(struct rt *R, int threads)
         delete c;
         return -1;
     }
+    /* the environment, read here once */
     const char *ex = getenv("Q8_EXACT");
     c->exact = ex && atoi(ex) != 0;
+    const char *ws = getenv("Q8_WAIT_S");
+    if (ws && atof(ws) > 0.0)
+        c->wait_s = atof(ws);
+    const char *uc = getenv("Q8_UPLOAD_CHUNK");
+    if (uc && atol(uc) > 0)
+        c->upload_chunk = (size_t)atol(uc);
+    const char *ae = getenv("Q8_ABORT_EXIT");
+    abort_exit = ae ? atoi(ae) : 0;
     /* R->team and R->frame belong to the caller, which creates its team before rt_init
      * (src/card/engine.c:249-250) and keeps using it for the primitives that are not products */
     R->gemm_chain = nullptr;
     R->chain = c;
     R->threads = threads;
+    live.push_back(c);
     current = c;
     return 0;
 }
@@ -544,7 +581,7 @@ void rt_fini(struct rt *R)
     if (!R || !R->chain)
         return;
     ctx *c = (ctx *)R->chain;
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_fini");
     for (auto &kv : c->weights)
         if (kv.second.owned)
             HIPCHECK(hipFree((void *)kv.first));
@@ -576,8 +613,12 @@ void rt_fini(struct rt *R)
         if (c->up_done[k])
             HIPCHECK(hipEventDestroy(c->up_done[k]));
     }
-    if (current == c)
-        current = nullptr;
+    for (size_t i = 0; i < live.size(); i++)
+        if (live[i] == c) {
+            live.erase(live.begin() + (long)i);
+            break;
+        }
+    current = live.empty() ? nullptr : live.back();
     HIPCHECK(hipEventDestroy(c->ev0));
     HIPCHECK(hipEventDestroy(c->ev1));
     HIPCHECK(hipStreamDestroy(c->stream));
@@ -592,7 +633,7 @@ void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, 
     if (!x || !y)
         fail("rt_gemv", "x and y must be host arrays");
     job j = {w, rows, cols, 1, x, y, 0, 0};
-    run_round(c, &j, 1);
+    run_round(c, &j, 1, "rt_gemv");
 }
 
 void rt_gemv_q(struct rt *R, const void *w, long rows, long cols, const float *x, float *y)
@@ -621,7 +662,7 @@ void rt_gemv_go(struct rt *R)
 {
     ctx *c = get(R, "rt_gemv_go");
     if (c->queued)
-        run_round(c, c->queue, c->queued);
+        run_round(c, c->queue, c->queued, "rt_gemv_go");
     c->queued = 0;
 }
 
@@ -632,7 +673,7 @@ void rt_gemm(struct rt *R, const void *w, long rows, long cols, const float *x, 
     if (t < 1)
         fail("rt_gemm", "t must be at least 1");
     job j = {w, rows, cols, t, x, y, 0, 0};
-    run_round(c, &j, 1);
+    run_round(c, &j, 1, "rt_gemm");
 }
 
 long gemv_i_bytes(long rows, long cols) { return rows / Q8_GROUP * (cols / Q8_BLOCK) * 544; }
@@ -663,21 +704,17 @@ static const void *register_matrix(ctx *c, void *dev, long rows, long cols, bool
 }
 
 extern "C++" {
-/* Bytes of an upload chunk: Q8_UPLOAD_CHUNK (bytes) or 64 MiB; at least one 16-row group. */
-static size_t upload_chunk(size_t group)
-{
-    const char *v = getenv("Q8_UPLOAD_CHUNK");
-    size_t n = v && atol(v) > 0 ? (size_t)atol(v) : (size_t)64 << 20;
-    return n < group ? group : n;
-}
+/* Bytes of an upload chunk: the runtime's setting (64 MiB unless Q8_UPLOAD_CHUNK or
+ * rt_set_upload_chunk says otherwise), at least one 16-row group. */
+static size_t upload_chunk(const ctx *c, size_t group) { return c->upload_chunk < group ? group : c->upload_chunk; }
 
 static void reserve_upload(ctx *c, size_t group)
 {
-    const size_t need = upload_chunk(group);
+    const size_t need = upload_chunk(c, group);
     if (c->up_cap >= need)
         return;
     no_capture(c, "the upload staging");
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "the upload staging");
     for (int k = 0; k < 2; k++) {
         if (c->up_host[k])
             HIPCHECK(hipHostFree(c->up_host[k]));
@@ -702,16 +739,16 @@ static const void *upload_groups(ctx *c, const char *fn, long rows, long cols, R
     no_capture(c, fn);
     const size_t bytes = (size_t)gemv_i_bytes(rows, cols), group = (size_t)gemv_i_bytes(Q8_GROUP, cols);
     reserve_upload(c, group);
-    const size_t want = upload_chunk(group), per = (want < c->up_cap ? want : c->up_cap) / group * group;
+    const size_t want = upload_chunk(c, group), per = (want < c->up_cap ? want : c->up_cap) / group * group;
     void *out = nullptr;
     if (hipMalloc(&out, bytes) != hipSuccess)
         return nullptr;
     int k = 0;
     for (size_t off = 0; off < bytes; off += per, k ^= 1) {
         const size_t n = bytes - off < per ? bytes - off : per;
-        HIPCHECK(hipEventSynchronize(c->up_done[k])); /* the slot's last copy has read its chunk */
+        sync_event(c, c->up_done[k], fn); /* the slot's last copy has read its chunk */
         if (!read(c->up_host[k], off, n)) {
-            HIPCHECK(hipStreamSynchronize(c->stream));
+            sync_stream(c, fn);
             HIPCHECK(hipFree(out));
             *read_failed = true;
             return nullptr;
@@ -721,7 +758,7 @@ static const void *upload_groups(ctx *c, const char *fn, long rows, long cols, R
         launched("the repack");
         HIPCHECK(hipEventRecord(c->up_done[k], c->stream));
     }
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, fn);
     return register_matrix(c, out, rows, cols);
 }
 } /* extern "C++" */
@@ -774,7 +811,7 @@ const void *rt_q8_upload_packed(struct rt *R, const void *packed, long rows, lon
     if (hipMalloc(&out, bytes) != hipSuccess)
         return nullptr;
     HIPCHECK(hipMemcpyAsync(out, packed, bytes, hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_q8_upload_packed");
     return register_matrix(c, out, rows, cols);
 }
 
@@ -786,7 +823,7 @@ void rt_q8_free(struct rt *R, const void *w)
         fail("rt_q8_free", "w is not a handle from rt_q8_upload");
     if (!it->second.owned)
         fail("rt_q8_free", "w is a buffer of the caller's that rt_q8_repack_dev registered: free it with rt_dev_free");
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_q8_free");
     HIPCHECK(hipFree((void *)w));
     c->weights.erase(it);
 }
@@ -905,7 +942,7 @@ void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const lon
         check_dev_ptr("rt_gemv_round_norm_dev", y[i], "every y");
     }
     const q8_stream_t s = (q8_stream_t)c->stream;
-    if (!c->exact && t <= 4 && !epi_apart()) {
+    if (!c->exact && t <= 4 && !c->epi_apart) {
         long total = 0;
         for (int i = 0; i < n; i++)
             total += rows[i];
@@ -949,13 +986,25 @@ void *rt_dev_alloc(struct rt *R, long bytes)
 void rt_dev_free(struct rt *R, void *p)
 {
     ctx *c = get(R, "rt_dev_free");
+    if (!p)
+        return;
     auto it = c->weights.find(p);
-    if (it != c->weights.end()) {
-        if (it->second.owned)
-            fail("rt_dev_free", "p is a weight handle the library allocated: free it with rt_q8_free");
-        c->weights.erase(it); /* a buffer rt_q8_repack_dev registered stops being a handle */
+    if (it != c->weights.end() && it->second.owned)
+        fail("rt_dev_free", "p is a weight handle the library allocated: free it with rt_q8_free");
+    /* every buffer rt_q8_repack_dev registered inside the allocation stops being a handle, the
+     * allocation's start or an address inside it */
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    HIPCHECK(hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p));
+    const uintptr_t lo = (uintptr_t)base, hi = lo + size;
+    for (auto w = c->weights.begin(); w != c->weights.end();) {
+        const uintptr_t a = (uintptr_t)w->first;
+        if (!w->second.owned && a >= lo && a < hi)
+            w = c->weights.erase(w);
+        else
+            ++w;
     }
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_dev_free");
     HIPCHECK(hipFree(p));
 }
 
@@ -963,17 +1012,21 @@ void rt_dev_upload(struct rt *R, void *dst, const void *src, long bytes)
 {
     ctx *c = get(R, "rt_dev_upload");
     HIPCHECK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, c->stream));
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_dev_upload");
 }
 
 void rt_dev_download(struct rt *R, void *dst, const void *src, long bytes)
 {
     ctx *c = get(R, "rt_dev_download");
     HIPCHECK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, c->stream));
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_dev_download");
 }
 
-void rt_dev_sync(struct rt *R) { HIPCHECK(hipStreamSynchronize(get(R, "rt_dev_sync")->stream)); }
+void rt_dev_sync(struct rt *R)
+{
+    ctx *c = get(R, "rt_dev_sync");
+    sync_stream(c, "rt_dev_sync");
+}
 
 void rt_q8_fill_dev(struct rt *R, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma)
 {
@@ -989,9 +1042,15 @@ void rt_q8_repack_dev(struct rt *R, const void *q8_dev, long rows, long cols, vo
     ctx *c = get(R, "rt_q8_repack_dev");
     if (!q8_dev || !out_dev || rows <= 0 || cols <= 0 || rows % Q8_GROUP || cols % Q8_BLOCK || ((uintptr_t)out_dev & 31) || ((uintptr_t)q8_dev & 1))
         fail("rt_q8_repack_dev", "needs rows a positive multiple of 16, cols of 32, out 32-byte aligned");
-    auto it = c->weights.find(out_dev);
+    /* out_dev must not lie in a matrix the library allocated: its start or an address inside it */
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    HIPCHECK(hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)out_dev));
+    auto it = c->weights.find((const void *)base);
     if (it != c->weights.end() && it->second.owned)
-        fail("rt_q8_repack_dev", "out_dev is a weight handle the library allocated");
+        fail("rt_q8_repack_dev", "out_dev lies in a weight handle the library allocated");
+    if ((uintptr_t)out_dev + (size_t)gemv_i_bytes(rows, cols) > (uintptr_t)base + size)
+        fail("rt_q8_repack_dev", "out_dev's allocation ends before the repacked matrix does");
     q8_launch_repack((q8_stream_t)c->stream, q8_dev, rows, cols, out_dev);
     launched("the repack");
     register_matrix(c, out_dev, rows, cols, false);
@@ -1024,7 +1083,7 @@ void rt_q8_row(const void *w, long cols, long row, float *z)
     launched("the copy of the row index");
     q8_launch_rows((q8_stream_t)c->stream, w, cols, it->second.rows, dr, 1, c->hy);
     launched("the row read");
-    wait_done(c);
+    wait_done(c, "rt_q8_row");
     memcpy(z, c->hy, sizeof(float) * (size_t)cols);
 }
 
@@ -1088,6 +1147,32 @@ int rt_set_exact(struct rt *R, int exact)
     return old;
 }
 
+int rt_set_epi_apart(struct rt *R, int apart)
+{
+    ctx *c = get(R, "rt_set_epi_apart");
+    const int old = c->epi_apart;
+    c->epi_apart = apart != 0;
+    return old;
+}
+
+long rt_set_upload_chunk(struct rt *R, long bytes)
+{
+    ctx *c = get(R, "rt_set_upload_chunk");
+    if (bytes <= 0)
+        fail("rt_set_upload_chunk", "bytes must be positive");
+    const long old = (long)c->upload_chunk;
+    c->upload_chunk = (size_t)bytes;
+    return old;
+}
+
+void rt_gemm_force(struct rt *R, int streaming, int ks)
+{
+    ctx *c = get(R, "rt_gemm_force");
+    if (ks < 0)
+        fail("rt_gemm_force", "ks must be 0 (the planner's) or a split count");
+    c->gemm_opts = q8_gemm_opts{ks, streaming != 0};
+}
+
 void rt_timer_start(struct rt *R)
 {
     ctx *c = get(R, "rt_timer_start");
@@ -1099,7 +1184,7 @@ float rt_timer_stop(struct rt *R)
     ctx *c = get(R, "rt_timer_stop");
     float ms = 0.0f;
     HIPCHECK(hipEventRecord(c->ev1, c->stream));
-    HIPCHECK(hipEventSynchronize(c->ev1));
+    sync_event(c, c->ev1, "rt_timer_stop");
     HIPCHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
     return ms;
 }
@@ -1132,7 +1217,7 @@ void rt_graph_launch(struct rt *R, void *graph)
 void rt_graph_free(struct rt *R, void *graph)
 {
     ctx *c = get(R, "rt_graph_free");
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_graph_free");
     HIPCHECK(hipGraphExecDestroy((hipGraphExec_t)graph));
 }
 
@@ -1152,7 +1237,7 @@ void rt_ktime(struct rt *R, int on)
 long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, char *names, long *grid, long max)
 {
     ctx *c = get(R, "rt_ktime_read");
-    HIPCHECK(hipStreamSynchronize(c->stream));
+    sync_stream(c, "rt_ktime_read");
     const long n = (long)c->kt.size() < max ? (long)c->kt.size() : max;
     for (long i = 0; i < n; i++) {
         float ms = 0.0f;

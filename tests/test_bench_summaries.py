@@ -100,7 +100,7 @@ def test_verify_summary_per_kernel_and_grid(tmp_path):
     XCDs, 1024 SIMDs, SQ_WAVE_CYCLES and SQ_WAIT_INST_ANY in quad-cycles)."""
     run = tmp_path / "run"
     F, H = bench.FFN, bench.HIDDEN
-    pk, dk = "gemv_mx<4, 4, 1, 4, 1, 0>", "gemv_mx<4, 12, 0, 4, 2, 0>"
+    pk, dk = "gemv_k<4, 8, 1, 4, 1>", "gemv_k<4, 16, 1, 12, 0>"
     line = {"verify": {"M4": {"fused_gate_up": {"kernel_us": 30.0, "kernel": pk, "grid": 196608},
                               "down": {"kernel_us": 20.0, "kernel": dk, "grid": 196608}}}}
     os.makedirs(run)

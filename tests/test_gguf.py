@@ -292,3 +292,68 @@ def test_upload_refuses_bad_shapes_before_the_gpu(q8rt, tmp_path):
         assert lib.rt_gguf_upload(None, C.byref(g.h), os.fsencode(path), err, 512) == -1
         assert f"tensor {name}:" in err.value.decode() and want in err.value.decode(), err.value.decode()
         g.close()
+
+
+@pytest.mark.parametrize("vt,v", [(gf.STR, "64"), (gf.F32, 64.0), (gf.U64, 64), (gf.I32, 64), (gf.U8, 64), (gf.F64, 64.0)])
+def test_alignment_of_any_type_read_as_the_reference(q8rt, tmp_path, vt, v):
+    """general.alignment is read as the reference reads it, strtoull of the key's text
+    (gguf_reader.c:198-202), whatever the key's type: 64 as a string, a float or any integer type
+    puts the data on the writer's 64-byte boundary, as the reference's reader does."""
+    keys = [("general.architecture", gf.STR, "qwen35"), ("general.alignment", vt, v)]
+    path = tmp_path / "a.gguf"
+    info = gf.write(path, keys, TENSORS_ALL, alignment=64)
+    ours, e = our_read(q8rt, path)
+    assert e is None, e
+    assert ours[0]["data_start"] == info["data_start"] and info["data_start"] % 64 == 0
+    assert [t["offset"] for t in ours[2]] == [info["offsets"][t["name"]] for t in TENSORS_ALL]
+
+
+def test_alignment_of_any_type_matches_reference_reader(q8rt, ref_gguf, tmp_path):
+    for i, (vt, v) in enumerate([(gf.STR, "64"), (gf.F32, 64.0), (gf.I16, 64), (gf.STR, "4096")]):
+        keys = [("general.architecture", gf.STR, "qwen35"), ("general.alignment", vt, v)]
+        path = tmp_path / f"a{i}.gguf"
+        gf.write(path, keys, TENSORS_ALL, alignment=int(float(v)))
+        ours, e1 = our_read(q8rt, path)
+        ref, e2 = ref_read(ref_gguf, path)
+        assert e1 is None and e2 is None, (e1, e2)
+        assert ours[0] == ref[0] and ours[2] == ref[2], (vt, v)
+
+
+def _raw_header(offset, alignment_key=None):
+    """GGUF v3 bytes: optionally a general.alignment key (type, value), then one Q8_0 tensor of 16 x 32
+    (544 bytes) at the given offset from the data start; a little data after the header."""
+    nkeys = 1 if alignment_key else 0
+    head = b"GGUF" + struct.pack("<IQQ", 3, 1, nkeys)
+    if alignment_key:
+        head += gf.key("general.alignment", *alignment_key)
+    head += gf.gstr("blk.0.w.weight") + struct.pack("<I", 2) + struct.pack("<QQ", 32, 16) + struct.pack("<IQ", gf.Q8_0, offset)
+    return head + bytes(64)
+
+
+@pytest.mark.parametrize("offset", [2**64 - 32, 2**64 - 544])
+def test_offset_past_2_64_refused(q8rt, tmp_path, offset):
+    """A tensor whose offset + size wraps 64 bits (the reference's sums would wrap and pass its size
+    checks) is refused with the tensor's name."""
+    path = tmp_path / "wrap.gguf"
+    path.write_bytes(_raw_header(offset))
+    _, e = our_read(q8rt, path)
+    assert e is not None and "blk.0.w.weight" in e and "overflows 64 bits" in e, e
+
+
+def test_data_end_past_2_64_refused(q8rt, tmp_path):
+    """An offset whose end fits in 64 bits (2^64 - 32) but lands past 2^64 once the data start (96
+    here) is added is refused."""
+    path = tmp_path / "wrap2.gguf"
+    path.write_bytes(_raw_header(2**64 - 576))
+    _, e = our_read(q8rt, path)
+    assert e is not None and "past 2^64 bytes" in e, e
+
+
+@pytest.mark.parametrize("key", [(gf.I8, -1), (gf.I64, -32), (gf.U64, 2**64 - 1)])
+def test_alignment_past_2_64_refused(q8rt, tmp_path, key):
+    """A negative alignment key reads, as strtoull reads "-1", as 2^64 - 1: the data start would wrap,
+    so the file is refused."""
+    path = tmp_path / "al.gguf"
+    path.write_bytes(_raw_header(0, key))
+    _, e = our_read(q8rt, path)
+    assert e is not None and "general.alignment" in e and "past 2^64 bytes" in e, e

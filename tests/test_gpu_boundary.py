@@ -46,19 +46,43 @@ CHILD = textwrap.dedent(
     elif case == "freed":
         rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
         rt.gemv_q(w, rows, cols, x, y)
+    elif case in ("sub_freed", "sub_live"):
+        # a matrix repacked into a buffer inside a larger allocation, at an offset
+        blk, src = rt.alloc(4 * q8.nbytes), rt.alloc(q8.nbytes)
+        rt.to_dev(src, q8)
+        sub = blk + 4096
+        rt.lib.rt_q8_repack_dev(rt.R, c.c_void_p(src), rows, cols, c.c_void_p(sub))
+        dx, dy = rt.alloc(4 * cols), rt.alloc(4 * rows)
+        rt.lib.rt_gemm_dev(rt.R, c.c_void_p(sub), rows, cols, c.c_void_p(dx), cols, 1, c.c_void_p(dy))  # a handle: fine
+        rt.sync()
+        if case == "sub_freed":
+            rt.free(blk)  # the allocation goes, and with it the handle inside it
+        print("child: calling with", case, flush=True)
+        rt.lib.rt_gemm_dev(rt.R, c.c_void_p(sub), rows, cols, c.c_void_p(dx), cols, 1, c.c_void_p(dy))
+        rt.sync()
+        if case == "sub_live":
+            print("child: live sub-buffer handle works", flush=True)
+            rt.lib.rt_q8_repack_dev(rt.R, c.c_void_p(src), rows, cols, c.c_void_p(w + 4096))
     print("child: returned", flush=True)
     """
 )
 
 
-@pytest.mark.parametrize("case", ["host", "device", "inside", "freed"])
+@pytest.mark.parametrize("case", ["host", "device", "inside", "freed", "sub_freed", "sub_live"])
 def test_unregistered_w_stops_before_launch(case):
+    """sub_freed: a buffer rt_q8_repack_dev registered at an offset inside an allocation stops being a
+    handle when rt_dev_free frees the allocation. sub_live: while the allocation lives it is a handle,
+    and a repack into a matrix the library allocated (at an address inside it) is refused."""
     env = dict(os.environ, Q8_ABORT_EXIT="42")
     r = subprocess.run([sys.executable, "-c", CHILD.format(root=ROOT), case], env=env, capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 42, (r.returncode, r.stderr)
     assert "child: calling with" in r.stdout and "child: returned" not in r.stdout
-    assert "is not a weight handle" in r.stderr
+    if case == "sub_live":
+        assert "child: live sub-buffer handle works" in r.stdout
+        assert "out_dev lies in a weight handle the library allocated" in r.stderr
+    else:
+        assert "is not a weight handle" in r.stderr
 
 
 def test_row_gather_bounds(rt, oracle):

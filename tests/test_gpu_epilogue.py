@@ -202,10 +202,8 @@ def test_layer_graph_with_epilogues(rt, oracle):
 
 
 def test_epilogues_apart_switch(rt, oracle):
-    """Q8_EPI_APART=1 runs the epilogues as kernels of their own: the residual's bits are the fused
-    ones, the norm product meets the bar (its sum in the separate kernel's order)."""
-    import os
-
+    """rt_set_epi_apart(R, 1) runs the epilogues as kernels of their own: the residual's bits are the
+    fused ones, the norm product meets the bar (its sum in the separate kernel's order)."""
     rows, cols, t = 4096, 4096, 2
     q8, x = synth.case(909, rows, cols, t)
     nw = _vec(910, cols)
@@ -214,8 +212,7 @@ def test_epilogues_apart_switch(rt, oracle):
     out = {}
     try:
         for apart in (False, True):
-            if apart:
-                os.environ["Q8_EPI_APART"] = "1"
+            old = rt.set_epi_apart(apart)
             try:
                 with Dev(rt) as d:
                     dx, dn, dr, dy, dz = d.put(x), d.put(nw), d.put(r), d.empty(4 * t * rows), d.empty(4 * t * rows)
@@ -223,7 +220,7 @@ def test_epilogues_apart_switch(rt, oracle):
                     rt.lib.rt_gemm_norm_dev(rt.R, c.c_void_p(w), rows, cols, c.c_void_p(dx), cols, t, c.c_void_p(dn), EPS, c.c_void_p(dz))
                     out[apart] = (d.get(dy, (t, rows), np.float32), d.get(dz, (t, rows), np.float32))
             finally:
-                os.environ.pop("Q8_EPI_APART", None)
+                rt.set_epi_apart(old)
     finally:
         rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
     assert np.array_equal(out[False][0].view(np.uint32), out[True][0].view(np.uint32))

@@ -34,18 +34,13 @@ def test_gguf_upload_bytes_rows_products(rt, q8rt, oracle, tmp_path, chunk):
     keys, tensors, q8 = gf.model(23, SHAPES, alignment=64)
     path = tmp_path / "model.gguf"
     gf.write(path, keys, tensors, alignment=64)
-    old = os.environ.get("Q8_UPLOAD_CHUNK")
-    if chunk:
-        os.environ["Q8_UPLOAD_CHUNK"] = str(chunk)
+    old = rt.set_upload_chunk(chunk) if chunk else None
     try:
         g = q8rt.GGUF(path)
         g.upload(rt)
     finally:
         if chunk:
-            if old is None:
-                del os.environ["Q8_UPLOAD_CHUNK"]
-            else:
-                os.environ["Q8_UPLOAD_CHUNK"] = old
+            rt.set_upload_chunk(old)
     try:
         assert g.h.q8_count == len(SHAPES)
         assert g.h.q8_bytes == sum(r * k // 32 * 34 for r, k in SHAPES.values())
@@ -99,16 +94,12 @@ def test_gguf_upload_fd_reads_at_offset(rt, q8rt, oracle, tmp_path):
     path = tmp_path / "raw.bin"
     path.write_bytes(b"\x07" * 1001 + q8.tobytes() + b"\x09" * 17)
     fd = os.open(path, os.O_RDONLY)
-    old = os.environ.get("Q8_UPLOAD_CHUNK")
-    os.environ["Q8_UPLOAD_CHUNK"] = str(3 * 16 * cols // 32 * 34)
+    old = rt.set_upload_chunk(3 * 16 * cols // 32 * 34)
     try:
         w = rt.lib.rt_q8_upload_fd(rt.R, fd, 1001, rows, cols)
     finally:
         os.close(fd)
-        if old is None:
-            del os.environ["Q8_UPLOAD_CHUNK"]
-        else:
-            os.environ["Q8_UPLOAD_CHUNK"] = old
+        rt.set_upload_chunk(old)
     assert w
     try:
         assert np.array_equal(_device_bytes(rt, w, q8.size), oracle.repack_s(q8, rows, cols))

@@ -134,9 +134,8 @@ def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
             y = h.product(X[:t], exact=True)
             assert np.array_equal(y.view(np.uint32), one_exact[:t].view(np.uint32)), f"reference order t={t}"
         worst = 0.0
-        for ks in ("", "1", "3"):
-            if ks:
-                os.environ["Q8_GEMM_KS"] = ks
+        for ks in (0, 1, 3):
+            rt.gemm_force(ks=ks)
             try:
                 for t in (3, 4, 5, 16, 17, 40):
                     y = h.product(X[:t])
@@ -144,8 +143,37 @@ def test_batch_deviation_is_bounded(rt, oracle, rows, cols):
                     assert_parity(y, f64[:t], f"t={t} ks={ks or 'planned'} against F64")
                     worst = max(worst, m["max_rel"])
             finally:
-                os.environ.pop("Q8_GEMM_KS", None)
+                rt.gemm_force()
         say(f"{rows}x{cols}: largest max-rel between gemm(t)[k] and gemv(x[k]) at t >= 3: {worst:.3e}")
+    finally:
+        h.close()
+
+
+MC_T = (5, 16, 17, 40, 64, 65, 70)
+
+
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (4096, 12288), (151936, 4096)])
+def test_matrix_core_bits_independent_of_t(rt, oracle, rows, cols):
+    """On the matrix cores (t >= 5) a token's output has the same bits whatever the number of tokens
+    it was computed with: the K split is a function of the matrix's shape alone, and every 64-token
+    launch of a longer X, the last one too however few tokens it holds, runs on the matrix cores.
+    The 9B FFN shapes (one token tile on the x-resident kernel, two to four on the streaming one) and
+    the output head (whose K split the workspace limits); 65 tokens end in a one-token launch."""
+    h = Handle(rt, rows, cols, seed=3 * rows + cols)
+    head = rows == VOCAB
+    try:
+        n = 17 if head else max(MC_T)
+        X = np.random.default_rng(rows + 2 * cols).standard_normal((n, cols), dtype=np.float32)
+        full = h.product(X)
+        for t in MC_T:
+            if t > n:
+                continue
+            say(f"{rows}x{cols} t={t} against t={n}")
+            y = h.product(X[:t])
+            assert np.array_equal(y.view(np.uint32), full[:t].view(np.uint32)), f"{rows}x{cols}: t={t} differs from t={n}"
+        # the F64 closed form of the head at 17 tokens is minutes of CPU: its parity is test_head_parity's
+        if not head:
+            assert_parity(full, oracle.gemm_f64(h.q8, rows, cols, X), f"{rows}x{cols} t={n}")
     finally:
         h.close()
 

@@ -243,52 +243,46 @@ def test_matrix_core_gemm_deterministic(rt):
         assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
 
 
-class env:
-    """Environment variables set for a block (the GEMM planner reads Q8_GEMM_CFG and Q8_GEMM_KS at
-    every product)."""
+class force:
+    """The matrix-core product's K split (ks > 0) and, with streaming, its streaming kernel for one
+    token tile, for a block (rt_gemm_force; the planner's choices again after it)."""
 
-    def __init__(self, **kv):
-        self.kv, self.old = kv, {}
+    def __init__(self, rt, streaming=False, ks=0):
+        self.rt, self.streaming, self.ks = rt, streaming, ks
 
     def __enter__(self):
-        for k, v in self.kv.items():
-            self.old[k] = os.environ.get(k)
-            os.environ[k] = v
+        self.rt.gemm_force(self.streaming, self.ks)
 
     def __exit__(self, *e):
-        for k, v in self.old.items():
-            if v is None:
-                del os.environ[k]
-            else:
-                os.environ[k] = v
+        self.rt.gemm_force()
 
 
 @pytest.mark.parametrize("rows,cols,t", [(12288, 4096, 16), (4096, 12288, 9), (1888, 1056, 5), (48, 4096, 13)])
 def test_x_resident_gemm_equals_streaming(rt, oracle, rows, cols, t):
     """One token tile: the x-resident kernel (the default at t <= 16) and the streaming kernel with
-    the same ranges (Q8_GEMM_CFG=1,1,2,16) give the same bits on the same K split. Q8_GEMM_KS=1
+    the same ranges (gemm_mfma<1, 1, 2, 16>) give the same bits on the same K split. One K split
     gives the x-resident kernel several LDS segments (every range of K in one workgroup: 4, 12 and
     2 segments here) and stores Y directly; 1056 columns end on half a pair; 1888 and 48 rows leave
     waves past the last row tile."""
     q8, x = synth.case(5 * rows + cols + t, rows, cols, t)
     w = rt.upload(q8, rows, cols)
     try:
-        for ks in ("", "1", "3"):
-            with env(Q8_GEMM_KS=ks):
+        for ks in (0, 1, 3):
+            with force(rt, ks=ks):
                 say("x-resident gemm", rows, cols, t, "ks", ks or "planned")
                 a = gpu_gemm(rt, q8, rows, cols, x, w=w)
-                with env(Q8_GEMM_CFG="1,1,2,16"):
-                    b = gpu_gemm(rt, q8, rows, cols, x, w=w)
+            with force(rt, streaming=True, ks=ks):
+                b = gpu_gemm(rt, q8, rows, cols, x, w=w)
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"ks {ks or 'planned'}"
             assert_parity(a, oracle.gemm_f64(q8, rows, cols, x), f"{rows}x{cols} t={t} ks {ks or 'planned'}")
     finally:
         rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
-@pytest.mark.parametrize("ks", ["", "1"])
+@pytest.mark.parametrize("ks", [0, 1])
 def test_x_resident_gemm_strided_x_and_residual(rt, ks):
     """x rows wider than the product (x_stride > cols) give the contiguous x's bits, and the residual
-    epilogue, fused into the x-resident kernel's store (Q8_GEMM_KS=1) or into the partial sum, is
+    epilogue, fused into the x-resident kernel's store (one K split) or into the partial sum, is
     the product plus one F32 add."""
     rows, cols, t, xs = 1024, 2048, 7, 2048 + 96
     q8, x = synth.case(4242, rows, cols, t)
@@ -297,7 +291,7 @@ def test_x_resident_gemm_strided_x_and_residual(rt, ks):
     r = np.random.default_rng(5).standard_normal((t, rows)).astype(np.float32)
     w = rt.upload(q8, rows, cols)
     try:
-        with env(Q8_GEMM_KS=ks), Dev(rt) as d:
+        with force(rt, ks=ks), Dev(rt) as d:
             plain = gpu_gemm(rt, q8, rows, cols, x, w=w)
             dx, dr, dy = d.put(wide), d.put(r), d.empty(4 * t * rows)
             rt.lib.rt_gemm_dev(rt.R, c.c_void_p(w), rows, cols, c.c_void_p(dx), xs, t, c.c_void_p(dy))
