@@ -148,6 +148,19 @@ def token_9b(b):
             b.gemm(L["down"], HIDDEN, FFN, h, 1, yd)
         b.gemm(head, VOCAB, HIDDEN, xh, 1, logits)
 
+    sink = b.vec(VOCAB)  # a word a workgroup of the largest grid
+    V = c.c_void_p
+
+    def floor():
+        """the same 129 positions, each the product's loads on its grid and nothing else (rt_q8_read_dev)"""
+        for L in layers:
+            b.lib.rt_q8_read_dev(b.R, V(L["qkv"]), None, QKV, HIDDEN, V(xh), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["out"]), None, HIDDEN, HIDDEN, V(xa), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["gate"]), V(L["up"]), FFN, HIDDEN, V(xh), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["down"]), None, HIDDEN, FFN, V(h), V(sink))
+        b.lib.rt_q8_read_dev(b.R, V(head), None, VOCAB, HIDDEN, V(xh), V(sink))
+
+    token.floor = floor
     per_token = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) +
                           alg_bytes(HIDDEN, FFN, 1)) + alg_bytes(VOCAB, HIDDEN, 1)
     return layers, head, token, per_token
@@ -164,12 +177,15 @@ def token_trace(b):
     duration and the gap from its end to the next kernel's begin. Also each replay's own time on the
     stream's events, beside the trace's."""
     layers, head, token, per_token = token_9b(b)
-    b.lib.rt_graph_begin(b.R)
-    token()
-    graph = b.lib.rt_graph_end(b.R)
-    run = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(graph))  # noqa: E731
+    graphs = []
+    for fn in (token, token.floor):
+        b.lib.rt_graph_begin(b.R)
+        fn()
+        graphs.append(b.lib.rt_graph_end(b.R))
+    run = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(graphs[0]))  # noqa: E731
+    run_floor = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(graphs[1]))  # noqa: E731
     out = {"replays": TRACE_REPLAYS, "products": 4 * LAYERS + 1, "bytes_per_token": per_token}
-    for key, fn in (("graph", run), ("eager", token)):
+    for key, fn in (("graph", run), ("eager", token), ("floor", run_floor)):
         fn()
         b.rt.sync()
         ms = []
@@ -177,7 +193,8 @@ def token_trace(b):
             ms.append(b.timed(fn, 1))
         out[key] = {"ms_median": round(statistics.median(ms), 4), "ms_min": round(min(ms), 4)}
         log(f"  {key}: {out[key]}")
-    b.lib.rt_graph_free(b.R, c.c_void_p(graph))
+    for g in graphs:
+        b.lib.rt_graph_free(b.R, c.c_void_p(g))
     for L in layers:
         for w in L.values():
             b.rt.free(w)
@@ -206,6 +223,19 @@ def decode_9b(b, steps, warmup):
     ms_graph = b.timed(run, steps)
     ms_eager = b.timed(token, max(1, steps // 4))
     log(f"  token: graph {ms_graph:.3f} ms, eager {ms_eager:.3f} ms")
+    # the floor: the same 129 positions as pure reads on the products' grids, one graph
+    b.lib.rt_graph_begin(b.R)
+    token.floor()
+    fgraph = b.lib.rt_graph_end(b.R)
+    frun = lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(fgraph))  # noqa: E731
+    for _ in range(max(warmup, 5)):
+        frun()
+    b.floor_ms = b.timed(frun, steps)
+    b.floor_kernels = {}
+    for (kind, rows, cols, t), v in sorted(b.ktimes(token.floor, min(steps, 100)).items()):
+        b.floor_kernels[f"{kind} {rows}x{cols} t{t}"] = round(statistics.fmean(v), 3)
+    b.lib.rt_graph_free(b.R, c.c_void_p(fgraph))
+    log(f"  floor (pure reads on the same grids): graph {b.floor_ms:.3f} ms; {b.floor_kernels}")
     kt = b.ktimes(token, min(steps, 100))
     b.lib.rt_graph_free(b.R, c.c_void_p(graph))
     kernels = {}
@@ -215,6 +245,7 @@ def decode_9b(b, steps, warmup):
         gbs = alg_bytes(rows, cols, t, pair) / mean / 1e3
         kname, grid = b.knames[(kind, rows, cols, t)]
         kernels[f"{kind} {rows}x{cols} t{t}"] = {"us": round(mean, 3), "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                                                 "floor_us": b.floor_kernels.get(f"{kind} {rows}x{cols} t{t}"),
                                                  "launches": len(v), "kernel": kname, "grid": grid, "alg_bytes": alg_bytes(rows, cols, t, pair)}
         log(f"  {kind:9s} {rows:6d}x{cols:<5d} t{t}: {mean:8.2f} us  {gbs:7.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM)")
     # the dominant kernel: the most time per token
@@ -971,22 +1002,24 @@ def summarize_trace(run_dir, out=TRACE_PROFILE):
     rows = []
     for r in csv.DictReader(open(os.path.join(run_dir, "ttrace", "run_kernel_trace.csv"))):
         k = _kname(r["Kernel_Name"])
-        if k.startswith(("gemv_", "gemm_")):
+        if k.startswith(("gemv_", "gemm_", "read_k")):
             g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
             rows.append((k, g, int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     rows.sort(key=lambda r: r[2])
     runs = _replays(rows, n, VOCAB // 8 * 256)
     per = TRACE_REPLAYS + 1  # the untimed one first
-    if len(runs) != 2 * per:
-        raise SystemExit(f"summarize_trace: found {len(runs)} runs of {n} kernels, expected {2 * per}")
+    if len(runs) != 3 * per:
+        raise SystemExit(f"summarize_trace: found {len(runs)} runs of {n} kernels, expected {3 * per}")
     text = ["# The 9B decode token kernel by kernel: one graph replay in the kernel trace (rocprofv3)", "",
             f"Workload: the 9B-class decode token at M = 1, {n} products ({LAYERS} x (QKV 6144x4096, out 4096x4096, gate+up 2x12288x4096 "
             f"fused, down 4096x12288) + head 151936x4096), {line['bytes_per_token']} B a token, recorded once as a HIP graph. "
-            f"{TRACE_REPLAYS} replays, each alone on the stream (idle before and after), then {TRACE_REPLAYS} eager tokens the same way; "
-            "the first of each, untimed, is left out.", "",
+            f"{TRACE_REPLAYS} replays, each alone on the stream (idle before and after), then {TRACE_REPLAYS} eager tokens the same way, "
+            f"then {TRACE_REPLAYS} replays of the floor: a graph of the same 129 positions, each the product's loads on the product's grid "
+            "and no arithmetic (rt_q8_read_dev); the first of each, untimed, is left out.", "",
             "Commands (from the repository root):", "", "```"] + TRACE_PROFILE_CMDS + ["```", "",
             f"Each replay's time on the stream's events in the same run (under the trace): graph median {line['graph']['ms_median']} ms "
-            f"(min {line['graph']['ms_min']}), eager median {line['eager']['ms_median']} ms (min {line['eager']['ms_min']}).", ""]
+            f"(min {line['graph']['ms_min']}), eager median {line['eager']['ms_median']} ms (min {line['eager']['ms_min']}), floor median "
+            f"{line['floor']['ms_median']} ms (min {line['floor']['ms_min']}).", ""]
 
     def table(mode, group):
         spans = [(g[-1][3] - g[0][2]) / 1e3 for g in group]
@@ -1017,7 +1050,23 @@ def summarize_trace(run_dir, out=TRACE_PROFILE):
         text.append("")
 
     table("graph", runs[1:per])
-    table("eager", runs[per + 1:])
+    table("eager", runs[per + 1:2 * per])
+    table("floor", runs[2 * per + 1:])
+    # product against floor, position class by position class (the layer's four products and the head)
+    names = ["QKV 6144x4096", "out 4096x4096", "gate+up 2x12288x4096", "down 4096x12288"]
+    text.extend(["## Product against its floor", "", "Mean over every graph replay and floor replay of the kernel durations at each position "
+                 "of a layer (and the head): the product kernel, the pure read of the same bytes on the same grid, and the difference, "
+                 "which is the product's own arithmetic and reductions past its loads.", "",
+                 "| Position | Product us | Floor us | Product - floor us | Per token us |", "|---|---|---|---|---|"])
+    tot = [0.0, 0.0]
+    for j in range(5):
+        idx = [n - 1] if j == 4 else [4 * l + j for l in range(LAYERS)]
+        pd = statistics.fmean((g[i][3] - g[i][2]) / 1e3 for g in runs[1:per] for i in idx)
+        fd = statistics.fmean((g[i][3] - g[i][2]) / 1e3 for g in runs[2 * per + 1:] for i in idx)
+        tot[0] += pd * len(idx)
+        tot[1] += fd * len(idx)
+        text.append(f"| {names[j] if j < 4 else 'head 151936x4096'} | {pd:.3f} | {fd:.3f} | {pd - fd:.3f} | {(pd - fd) * len(idx):.1f} |")
+    text.extend(["", f"Kernel time a token: products {tot[0]:.1f} us, floor {tot[1]:.1f} us, difference {tot[0] - tot[1]:.1f} us.", ""])
     os.makedirs(os.path.dirname(out), exist_ok=True)
     open(out, "w").write("\n".join(text))
     print(f"wrote {out}")
@@ -1111,6 +1160,8 @@ def main():
                    "bytes_per_token": per_token, "products_per_token": 4 * LAYERS + 1},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "eager_ms_per_step": round(ms_eager, 4),
+        "floor_ms_per_step": round(b.floor_ms, 4),
+        "floor_pct_of_hbm_peak": round(100 * per_token / b.floor_ms / 1e6 / HBM_PEAK_GBS, 2),
         "gemm_m16_gflops": gm["GFLOPS"] if gm else None,
         "gemm_m16_mfma_util": gm["mfma_util_kernel"] if gm else None,
         "roofline": roof,

@@ -941,6 +941,83 @@ void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16)
     copy16<<<dim3((unsigned)((n16 + 255) / 256)), 256, 0, (hipStream_t)stream>>>((uint4 *)dst, (const uint4 *)src, n16);
 }
 
+/* The decode product's loads at one token and nothing else: the floor a product of that shape
+ * and grid cannot go below. Workgroup b of NW waves reads what gemv_k<1, RW, 1, NW, PAIR> reads for
+ * its rows [b*RW, +RW): x (the lane's 16 columns, four 16-byte loads), then each row's 16 bytes of
+ * weights and its binary16 scale (both matrices with PAIR), every load issued at once; the lane adds
+ * every 32-bit word it loaded (the scale zero-extended) into a wrapping sum, the wave's lanes are
+ * added, the NW waves' through LDS, and one thread stores the workgroup's sum to sink[blockIdx.x]:
+ * the product's own end (a sum over lanes and waves, one barrier, a store) without its arithmetic.
+ * The sums make the loads live and give a checksum the tests recompute. */
+template <int RW, int NW, int PAIR>
+__global__ __launch_bounds__(64 * NW) void read_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long cols, const float *__restrict__ x,
+                                                  unsigned *sink)
+{
+    constexpr int P = PAIR + 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long u0 = (long)wave * 64 + lane, r0 = (long)blockIdx.x * RW;
+    uint4 xv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        xv[c] = *(const uint4 *)(x + 16 * u0 + 4 * c);
+    uint4 q[RW][P];
+    uint16_t dh[RW][P];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const uint8_t *w = p ? w1 : w0;
+            q[r][p] = *(const uint4 *)(w + q8s_row_q(r0 + r, cols) + 16 * u0);
+            dh[r][p] = ((const uint16_t *)(w + q8s_row_d(r0 + r, cols)))[u0 >> 1];
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    unsigned acc = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        acc += xv[c].x + xv[c].y + xv[c].z + xv[c].w;
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < P; p++)
+            acc += q[r][p].x + q[r][p].y + q[r][p].z + q[r][p].w + (unsigned)dh[r][p];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        acc += (unsigned)__shfl_xor((int)acc, off, 64);
+    __shared__ unsigned red[NW];
+    if (lane == 0)
+        red[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned v = red[0];
+#pragma unroll
+        for (int k = 1; k < NW; k++)
+            v += red[k];
+        sink[blockIdx.x] = v;
+    }
+}
+
+/* the decode kernel's grid for a product at one token (gemv_choose), or false when the decode
+ * kernel would loop over K (cols not a multiple of 1024 in its instances) */
+int q8_launch_read(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, unsigned *sink)
+{
+    const long kb = cols % 1024 ? 0 : cols / 1024;
+    int rw, nw;
+    gemv_choose(w1 != nullptr, 1, rows, kb, &rw, &nw);
+    if (!kb || rows % rw || kb != nw)
+        return -1;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
+#define RD(RW_, NW_, P_)                                                                                               \
+    if (rw == RW_ && nw == NW_ && (b != nullptr) == (P_ == 1)) {                                                       \
+        Q8_LAUNCH(q8_time_name("read_k", 3, RW_, NW_, P_), (read_k<RW_, NW_, P_>), dim3((unsigned)(rows / RW_)), dim3(64 * NW_), s, a, b, cols, x,  \
+                  sink);                                                                                               \
+        return 0;                                                                                                      \
+    }
+    RD(8, 4, 0) RD(8, 12, 0) RD(4, 4, 1) RD(8, 2, 0) RD(4, 2, 0) RD(2, 2, 0) RD(4, 6, 0) RD(2, 6, 0) RD(2, 2, 1) RD(4, 2, 1) RD(8, 6, 0)
+#undef RD
+    return -1;
+}
+
 /* *flag = seq, stored by lane 0 with release order at system scope: the host sees it after every
  * store of the kernels before this one on the stream (each kernel's end writes back its stores). */
 __global__ void set_flag(unsigned *flag, unsigned seq)

@@ -1129,6 +1129,24 @@ void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes)
     launched("the copy");
 }
 
+void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, long cols, const float *x, unsigned *sink)
+{
+    ctx *c = get(R, "rt_q8_read_dev");
+    check_shape(c, "rt_q8_read_dev", w0, rows, cols);
+    if (w1)
+        check_shape(c, "rt_q8_read_dev", w1, rows, cols);
+    check_dev_ptr("rt_q8_read_dev", x, "x");
+    check_dev_ptr("rt_q8_read_dev", sink, "sink");
+    const bool timed = kt_begin(c, w1 ? RT_K_GEMV_PAIR : RT_K_GEMV, rows, cols, 1);
+    if (q8_launch_read((q8_stream_t)c->stream, w0, w1, rows, cols, x, sink) != 0) {
+        if (timed)
+            kt_cancel(c);
+        failf("rt_q8_read_dev", "no read kernel for %ld x %ld%s (the decode kernel's one-token grids, cols a multiple of 1024)", rows, cols,
+              w1 ? " (pair)" : "");
+    }
+    launched("the read");
+}
+
 void rt_prims_dev(struct rt *R, const int8_t *q, const float *x8, const float *c8, float *o8, long n8, const uint16_t *h, const float *xf,
                   const float *cf, float *of, long nf)
 {

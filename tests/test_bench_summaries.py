@@ -125,3 +125,41 @@ def test_verify_summary_per_kernel_and_grid(tmp_path):
         assert r[8] == "4.00" and r[10] == "1.000"  # VALU and MFMA instructions a weight
         assert r[11] == "10.0"                      # MFMA busy: 102400 / 1024000
         assert r[12] == "2.00" and r[13] == "25.0"  # waves a SIMD: 4 x 512000 / 1024000; waiting 128000 / 512000
+
+
+def test_trace_summary_replays_and_floor(tmp_path):
+    """bench.summarize_trace: the trace is cut into tokens at the head kernel (graph replays, eager tokens,
+    floor replays, in that order, the first of each left out); per position the product's and the
+    floor's mean durations and their difference come out as built, and the gap to the next kernel is
+    the next begin minus this end."""
+    run = tmp_path / "run"
+    n, per = 4 * bench.LAYERS + 1, bench.TRACE_REPLAYS + 1
+    head_grid = bench.VOCAB // 8 * 256
+    pos = [("gemv_k<1, 8, 1, 4, 0>", 196608, 6.0), ("gemv_k<1, 8, 1, 4, 0>", 131072, 5.0), ("gemv_k<1, 4, 1, 4, 1>", 786432, 18.0),
+           ("gemv_k<1, 8, 1, 12, 0>", 393216, 11.0)]
+    rows, t = [], 10**6
+    for mode in range(3):
+        for _ in range(per):
+            seq = [p for _ in range(bench.LAYERS) for p in pos] + [("gemv_k<1, 8, 1, 4, 0>", head_grid, 100.0)]
+            for name, grid, us in seq:
+                if mode == 2:
+                    name, us = "read_k<8, 4, 0>", us - 0.5  # the floor: half a microsecond less everywhere
+                rows.append({"Kernel_Name": f"void {name}(unsigned char const*, long)", "Grid_Size_X": grid, "Grid_Size_Y": 1,
+                             "Grid_Size_Z": 1, "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000)})
+                t += int(us * 1000) + 250  # 0.25 us from each end to the next begin
+            t += 10**6
+    _csv(str(run / "ttrace" / "run_kernel_trace.csv"), ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp",
+                                                         "End_Timestamp"], rows)
+    line = {"token_trace": {"replays": bench.TRACE_REPLAYS, "products": n, "bytes_per_token": 7228294656,
+                            **{k: {"ms_median": 1.4, "ms_min": 1.39} for k in ("graph", "eager", "floor")}}}
+    (run / "ttrace.log").write_text("noise\n" + json.dumps(line) + "\n")
+    out = tmp_path / "trace.md"
+    bench.summarize_trace(str(run), out=str(out))
+    text = out.read_text()
+    table = [[c.strip() for c in l.split("|")[1:-1]] for l in text.split("## Product against its floor")[1].splitlines() if l.startswith("| ")]
+    body = {r[0]: r for r in table[1:]}
+    assert body["QKV 6144x4096"][1:4] == ["6.000", "5.500", "0.500"]
+    assert body["gate+up 2x12288x4096"][1:5] == ["18.000", "17.500", "0.500", "16.0"]
+    assert body["head 151936x4096"][1:5] == ["100.000", "99.500", "0.500", "0.5"]
+    assert "0.250 us a boundary" in text
+    assert f"products {bench.LAYERS * 40.0 + 100.0:.1f} us, floor {bench.LAYERS * 38.0 + 99.5:.1f} us" in text

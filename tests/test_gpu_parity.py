@@ -677,3 +677,27 @@ def test_c_drop_in_caller(tmp_path):
     p = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     say(p.stdout)
     assert p.returncode == 0, p.stdout + p.stderr
+
+
+@pytest.mark.parametrize("rows,cols,pair", [(4096, 4096, False), (6144, 4096, False), (4096, 12288, False), (12288, 4096, True),
+                                            (3072, 2048, False), (6144, 2048, True), (2048, 6144, False), (151936, 4096, False)])
+def test_read_floor_checksum(rt, rows, cols, pair):
+    """rt_q8_read_dev (the decode product's loads on its grid, no arithmetic: the floor the benchmark
+    sets each product against) reads every byte of the matrix or matrices: its wrapping sum of the
+    32-bit words read equals numpy's, with x = 0 (each scale is read by two lanes)."""
+    rng = np.random.default_rng(rows + cols + pair)
+    mats = [synth.q8_rows(rng, rows, cols) for _ in range(2 if pair else 1)]
+    want = 0
+    for q8 in mats:
+        blk = q8.reshape(-1, 34)
+        want += int(blk[:, 2:].copy().view(np.uint32).astype(np.uint64).sum()) + 2 * int(blk[:, :2].copy().view(np.uint16).astype(np.uint64).sum())
+    ws = [rt.upload(q8, rows, cols) for q8 in mats]
+    try:
+        with Dev(rt) as d:
+            dx, sink = d.put(np.zeros(cols, np.float32)), d.put(np.zeros(rows, np.uint32))
+            rt.lib.rt_q8_read_dev(rt.R, c.c_void_p(ws[0]), c.c_void_p(ws[1]) if pair else None, rows, cols, c.c_void_p(dx), c.c_void_p(sink))
+            got = d.get(sink, (rows,), np.uint32)
+    finally:
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+    assert int(got.astype(np.uint64).sum()) % 2**32 == want % 2**32
