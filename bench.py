@@ -283,10 +283,11 @@ def draft_head(b):
     [b.gemm(w, DRAFT, HIDDEN, x, 1, y) for w in ws]  # one untimed pass
     kt = b.ktimes(lambda: [b.gemm(w, DRAFT, HIDDEN, x, 1, y) for w in ws], 4)
     us = statistics.fmean(next(iter(kt.values())))
+    kname, grid = b.knames[next(iter(kt))]
     for w in ws:
         b.rt.free(w)
     gb = alg_bytes(DRAFT, HIDDEN, 1)
-    return {"rows": DRAFT, "kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "copies": len(ws)}
+    return {"rows": DRAFT, "kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "copies": len(ws), "kernel": kname, "grid": grid}
 
 
 def prompt_gemm(b):
@@ -803,8 +804,18 @@ GEMM_PROFILE_CMDS = [
     "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/gprof_fetch -o run -- python3 bench.py --only prompt_gemm",
     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv "
     "-d gpurun_out/gprof_mfma -o run -- python3 bench.py --only prompt_gemm",
+    "rocprofv3 --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_VALU SQ_INSTS_VMEM_RD "
+    "SQ_INSTS_VALU GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/gprof_sq -o run -- python3 bench.py --only prompt_gemm,draft_head "
+    "> gpurun_out/gprof_sq.log 2>&1",
+    "rocprofv3 --pmc TA_TA_BUSY_sum TA_ADDR_STALLED_BY_TC_CYCLES_sum TD_TD_BUSY_sum TD_TC_STALL_sum TCP_TCP_TA_DATA_STALL_CYCLES_sum "
+    "TCP_PENDING_STALL_CYCLES_sum TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum GRBM_GUI_ACTIVE --output-format csv "
+    "-d gpurun_out/gprof_ta -o run -- python3 bench.py --only prompt_gemm,draft_head",
     "python3 bench.py --summarize-gemm gpurun_out",
 ]
+GEMM_STALL_COUNTERS = ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_VALU",
+                       "SQ_INSTS_VMEM_RD", "SQ_INSTS_VALU", "TA_TA_BUSY_sum", "TA_ADDR_STALLED_BY_TC_CYCLES_sum", "TD_TD_BUSY_sum",
+                       "TD_TC_STALL_sum", "TCP_TCP_TA_DATA_STALL_CYCLES_sum", "TCP_PENDING_STALL_CYCLES_sum", "TCP_TCC_READ_REQ_LATENCY_sum",
+                       "TCP_TCC_READ_REQ_sum")
 
 
 def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
@@ -821,9 +832,17 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
         g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
         trace[(_kname(r["Kernel_Name"]), g)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     cnt = defaultdict(lambda: defaultdict(list))
-    for sub in ("gprof_fetch", "gprof_mfma"):
-        for r in csv.DictReader(open(os.path.join(run_dir, sub, "run_counter_collection.csv"))):
-            cnt[(_kname(r["Kernel_Name"]), int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    stall = defaultdict(lambda: defaultdict(list))  # the two stall passes, each with its own GRBM_GUI_ACTIVE
+    for sub in ("gprof_fetch", "gprof_mfma", "gprof_sq", "gprof_ta"):
+        path = os.path.join(run_dir, sub, "run_counter_collection.csv")
+        if sub in ("gprof_sq", "gprof_ta") and not os.path.exists(path):
+            continue
+        for r in csv.DictReader(open(path)):
+            key = (_kname(r["Kernel_Name"]), int(r["Grid_Size"]))
+            if sub in ("gprof_sq", "gprof_ta"):
+                stall[key][(sub, r["Counter_Name"])].append(float(r["Counter_Value"]))
+            else:
+                cnt[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
     mean = lambda v: statistics.fmean(v) if v else float("nan")  # noqa: E731
     rows = []
     for shape, k in line.items():
@@ -854,6 +873,38 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512; issued = 2 x 3 limbs x the token tiles the kernel runs (whole groups of MG "
              "tiles of 16: at M = 40, 4 tiles, one of them all padding) x rows x cols. Counters are per (kernel, grid): "
              "products that launch the same kernel on the same grid share one average.", ""]
+    if stall:
+        dh = None
+        for l in open(os.path.join(run_dir, "gprof_sq.log")) if os.path.exists(os.path.join(run_dir, "gprof_sq.log")) else []:
+            if l.startswith('{"draft_head"'):
+                dh = json.loads(l)["draft_head"]
+        keyed = [(shape, (k["kernel"], k["grid"])) for shape, k in line.items()]
+        if dh and "kernel" in dh:
+            keyed.append((f"decode draft head {DRAFT}x{HIDDEN}, M=1 (contrast)", (dh["kernel"], dh["grid"])))
+        text += ["## Where the waves wait (two more counter passes)", "",
+                 f"Per kernel and grid, the kernel's cycles K = GRBM_GUI_ACTIVE / {xcds} of the same pass; a CU's TA, TD and TCP "
+                 f"count each on their own (256 of each; their _sum over the device / (256 x K) is the share of a unit's cycles); "
+                 f"SQ_WAVE_CYCLES and SQ_WAIT_INST_ANY are in quad-cycles (x 4). The draft head's decode kernel (1 KiB of one row "
+                 "a load instruction, every load of a wave issued at once) streams at 78 % of HBM: the contrast.", "",
+                 "| Product | Kernel | Waves a SIMD | Wave cycles waiting % | VMEM issue % | VALU issue % | TA busy % | TA stalled by TCP % | "
+                 "TD stalled by TCP % | TCP stalled on TA data % | TCP pending % | L2 read latency cycles | Loads a wave | "
+                 "VALU instructions a wave |", "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+        for shape, key in keyed:
+            st = stall.get(key, {})
+            g = lambda sub, n: mean(st.get((sub, n), []))  # noqa: E731
+            ksq, kta = g("gprof_sq", "GRBM_GUI_ACTIVE") / xcds, g("gprof_ta", "GRBM_GUI_ACTIVE") / xcds
+            cu = 256.0
+            waves = g("gprof_sq", "SQ_WAVES")
+            text.append(f"| {shape} | `{key[0]}` | {4 * g('gprof_sq', 'SQ_WAVE_CYCLES') / (ksq * simds):.2f} | "
+                        f"{100 * g('gprof_sq', 'SQ_WAIT_INST_ANY') / g('gprof_sq', 'SQ_WAVE_CYCLES'):.1f} | "
+                        f"{100 * g('gprof_sq', 'SQ_ACTIVE_INST_VMEM') / (ksq * simds):.1f} | "
+                        f"{100 * g('gprof_sq', 'SQ_ACTIVE_INST_VALU') / (ksq * simds):.1f} | "
+                        f"{100 * g('gprof_ta', 'TA_TA_BUSY_sum') / (cu * kta):.1f} | {100 * g('gprof_ta', 'TA_ADDR_STALLED_BY_TC_CYCLES_sum') / (cu * kta):.1f} | "
+                        f"{100 * g('gprof_ta', 'TD_TC_STALL_sum') / (cu * kta):.1f} | {100 * g('gprof_ta', 'TCP_TCP_TA_DATA_STALL_CYCLES_sum') / (cu * kta):.1f} | "
+                        f"{100 * g('gprof_ta', 'TCP_PENDING_STALL_CYCLES_sum') / (cu * kta):.1f} | "
+                        f"{g('gprof_ta', 'TCP_TCC_READ_REQ_LATENCY_sum') / g('gprof_ta', 'TCP_TCC_READ_REQ_sum'):.0f} | "
+                        f"{g('gprof_sq', 'SQ_INSTS_VMEM_RD') / waves:.1f} | {g('gprof_sq', 'SQ_INSTS_VALU') / waves:.0f} |")
+        text.append("")
     open(out, "w").write("\n".join(text))
     print(f"wrote {out}")
 

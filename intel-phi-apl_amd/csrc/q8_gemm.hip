@@ -84,8 +84,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
     constexpr int XN = MT * 2 * KP * 192; /* uint4 of x limbs in a range */
     __shared__ uint4 xls[2][XN];          /* two ranges: [tt][block in range][limb][lane] */
     __shared__ uint16_t dls[2][DN];       /* two ranges: [row of the workgroup][block in range] */
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const long nb = cols / Q8_BLOCK, nbp = (nb + 1) & ~1L, np = nbp / 2;
+    const int lane = threadIdx.x & 63;
+    /* the wave's index, uniform (see gemm_xres) */
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    /* block, pair and range indices in 32 bits (see gemm_xres) */
+    const int nb = (int)(cols / Q8_BLOCK), np = (nb + 1) / 2;
     const long tile = blockIdx.x / ks;
     const int split = (int)(blockIdx.x % ks);
     const long tt0 = (long)blockIdx.y * MT;
@@ -97,15 +100,16 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
     /* issue every load of the range starting at pair c0. All are unconditional, from indices
      * clamped to the matrix; what lies past t, past the last block or past the last pair is zeroed
      * after the loads (a load under a branch would make the wave wait for it before the next). */
-    auto issue = [&](stage &S, long c0) {
+    auto issue = [&](stage &S, int c0) {
         /* x of blocks [2*c0, 2*c0 + 2*KP) for token tiles [tt0, tt0 + MT) */
 #pragma unroll
         for (int k = 0; k < XR; k++) {
             const int i = (int)threadIdx.x + 64 * NW * k;
             const int L = i & 63, bb = (i >> 6) % (2 * KP), tt = (i >> 6) / (2 * KP);
-            const long tok = 16 * (tt0 + tt) + (L & 15), b = 2 * c0 + bb;
+            const long tok = 16 * (tt0 + tt) + (L & 15);
+            const int b = 2 * c0 + bb;
             S.xin[k] = (XS % (64 * NW) == 0 || i < XS) && tok < t && b < nb;
-            const float *px = x + (tok < t ? tok : t - 1) * x_stride + (b < nb ? b : nb - 1) * Q8_BLOCK + kcol(L >> 4);
+            const float *px = x + (tok < t ? tok : t - 1) * x_stride + (long)(b < nb ? b : nb - 1) * Q8_BLOCK + kcol(L >> 4);
             S.xr[k][0] = *(const float4 *)px;
             S.xr[k][1] = *(const float4 *)(px + 4);
         }
@@ -116,18 +120,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
             if (DN % (64 * NW) == 0 || i < DN) {
                 long row = tile * NW * RT * 16 + i / (2 * KP);
                 row = row < rows ? row : rows - 1;
-                long b = 2 * c0 + i % (2 * KP);
+                int b = 2 * c0 + i % (2 * KP);
                 b = b < nb ? b : nb - 1;
                 S.dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
             }
         }
 #pragma unroll
         for (int p = 0; p < KP; p++) {
-            const long c = c0 + p < np ? c0 + p : np - 1;
+            const int c = c0 + p < np ? c0 + p : np - 1;
 #pragma unroll
             for (int r = 0; r < RT; r++) {
-                const long row = live ? (rt0 + r) * 16 + n : n;
-                S.q[p][r] = *(const uint4 *)(w + q8s_row_q(row, cols) + 16 * kq + 64 * c);
+                /* the row tile at a uniform base, the lane's row and 16 bytes at a 32-bit offset */
+                const uint8_t *wt = w + q8s_row_q(live ? (rt0 + r) * 16 : 0, cols) + 64L * c;
+                S.q[p][r] = *(const uint4 *)(wt + (unsigned)(n * cols + 16 * kq));
             }
         }
     };
@@ -162,22 +167,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
         for (int m = 0; m < MT; m++)
             acc[r][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     /* the MFMAs of the range starting at pair c0, from LDS buffer bf and the stage's weights */
-    auto compute = [&](const stage &S, int bf, long c0) {
+    auto compute = [&](const stage &S, int bf, int c0) {
         const uint4 *xl = xls[bf];
         const uint16_t *dl = dls[bf];
 #pragma unroll
         for (int p = 0; p < KP; p++) {
-            const long c = c0 + p;
+            const int c = c0 + p;
             const bool ok0 = live && c < np, ok1 = live && 2 * c + 1 < nb; /* block 2c, block 2c+1 */
-            const bool keep = lane < 32 ? ok0 : ok1;
             bf16x8 wb[2][RT];
             float d[2][RT];
 #pragma unroll
             for (int r = 0; r < RT; r++) {
-                /* lanes 0-31 hold block 2c, 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
-                const uint32_t a0 = keep ? S.q[p][r].x : 0u, a1 = keep ? S.q[p][r].y : 0u, a2 = keep ? S.q[p][r].z : 0u, a3 = keep ? S.q[p][r].w : 0u;
-                const auto s02 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
-                const auto s13 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+                /* a block past the matrix needs no masking: its x limbs in LDS are zero and a bf16 weight is
+                 * finite, so its MFMAs give exactly 0 (its scale is zeroed below). Lanes 0-31 hold block 2c,
+                 * 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
+                const auto s02 = __builtin_amdgcn_permlane32_swap(S.q[p][r].x, S.q[p][r].z, false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap(S.q[p][r].y, S.q[p][r].w, false, false);
                 wb[0][r] = q8_bf16(s02[0], s13[0]);
                 wb[1][r] = q8_bf16(s02[1], s13[1]);
                 const int lr = (wave * RT + r) * 16 + n; /* the lane's row in the workgroup */
@@ -208,11 +213,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
      * range it loads that range again, from L2): under a branch, the wait before the commit
      * would also wait for the loads just issued. The scheduling barriers keep the compiler from
      * moving the loads off their place. */
-    const long r0 = (long)split * cps, nr = (np + KP - 1) / KP;
-    const int mine = (int)(nr - r0 < cps ? nr - r0 : cps); /* the last split may hold fewer ranges */
+    const int r0 = split * cps, nr = (np + KP - 1) / KP;
+    const int mine = nr - r0 < cps ? nr - r0 : cps; /* the last split may hold fewer ranges */
     for (int base = 0; base < mine; base += GEMM_CHUNK) {
         const int nc = mine - base < GEMM_CHUNK ? mine - base : GEMM_CHUNK;
-        const long rb = r0 + base;
+        const int rb = r0 + base;
         stage A, B;
         __builtin_amdgcn_sched_barrier(0);
         issue(A, rb * KP);
@@ -280,35 +285,42 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
     constexpr int DP = BS + 2;                          /* scale row pitch in LDS (halves): an odd dword count, no bank conflicts */
     __shared__ uint4 xls[BS * 3 * 64];                  /* [block][limb][lane] */
     __shared__ uint16_t dls[NW * 16 * DP];              /* [row of the workgroup][block] */
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const long nb = cols / Q8_BLOCK, np = (nb + 1) / 2;
+    const int lane = threadIdx.x & 63;
+    /* the wave's index, uniform: everything derived from it (the row tile, whether the wave is
+     * live, the range tests) stays in scalar registers */
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    /* block, pair and range indices in 32 bits: gfx9 compares 64-bit values only in vector registers */
+    const int nb = (int)(cols / Q8_BLOCK), np = (nb + 1) / 2;
     const long tile = blockIdx.x / ks;
     const int split = (int)(blockIdx.x % ks);
     const long rt0 = tile * NW + wave;
     /* a wave past the last row tile reads row tile 0 and contributes nothing */
     const bool live = rt0 < rows / 16;
     const int n = lane & 15, kq = lane >> 4;
-    const uint8_t *wq = w + q8s_row_q(live ? rt0 * 16 + n : n, cols) + 16 * kq;
+    /* the row tile's weights at a uniform base; the lane's row and 16 bytes at a 32-bit offset */
+    const uint8_t *wt = w + q8s_row_q(live ? rt0 * 16 : 0, cols);
+    const unsigned woff = (unsigned)(n * cols + 16 * kq);
 
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const long r0 = (long)split * cps, nr = (np + KP - 1) / KP;
-    const int mine = (int)(nr - r0 < cps ? nr - r0 : cps); /* the last split may hold fewer ranges */
+    const int r0 = split * cps, nr = (np + KP - 1) / KP;
+    const int mine = nr - r0 < cps ? nr - r0 : cps; /* the last split may hold fewer ranges */
     for (int sb = 0; sb < mine; sb += SC) {
         const int nc = mine - sb < SC ? mine - sb : SC;
-        const long c00 = (r0 + sb) * KP, b0 = 2 * c00; /* the segment's first pair and block */
+        const int c00 = (r0 + sb) * KP, b0 = 2 * c00; /* the segment's first pair and block */
         uint4 q[2][KP];
         float4 xr[XR][2];
         uint16_t dr[DR];
-        /* every load of the segment's x and scales, then range 0's weights, all unconditional from
-         * clamped indices (what lies past t or past the last block is zeroed after the loads) */
+        /* every load of the segment's x and scales, then ranges 0 and 1's weights, all unconditional
+         * from clamped indices (what lies past t or past the last block is zeroed after the loads):
+         * two ranges in flight while the x limbs are made, as during the stream */
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < XR; k++) {
             const int s = (int)threadIdx.x + 64 * NW * k;
             const int L = s & 63, bs = s >> 6, tok = L & 15;
-            long b = b0 + (bs < BS ? bs : BS - 1);
+            int b = b0 + (bs < BS ? bs : BS - 1);
             b = b < nb ? b : nb - 1;
-            const float *px = x + (tok < t ? tok : t - 1) * x_stride + b * Q8_BLOCK + kcol(L >> 4);
+            const float *px = x + (tok < t ? tok : t - 1) * x_stride + (long)b * Q8_BLOCK + kcol(L >> 4);
             xr[k][0] = *(const float4 *)px;
             xr[k][1] = *(const float4 *)(px + 4);
         }
@@ -317,16 +329,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
             const int s = (int)threadIdx.x + 64 * NW * k;
             long row = tile * NW * 16 + s / BS;
             row = row < rows ? row : rows - 1;
-            long b = b0 + s % BS;
+            int b = b0 + s % BS;
             b = b < nb ? b : nb - 1;
             dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < KP; p++) {
-            const long c = c00 + p < np ? c00 + p : np - 1;
-            q[0][p] = *(const uint4 *)(wq + 64 * c);
-        }
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int p = 0; p < KP; p++) {
+                int c = c00 + (h < nc ? h : nc - 1) * KP + p;
+                c = c < np ? c : np - 1;
+                q[h][p] = *(const uint4 *)(wt + 64L * c + woff);
+            }
         __builtin_amdgcn_sched_barrier(0);
         /* the segment's x limbs and scales into LDS (waits for them, not for the weights) */
 #pragma unroll
@@ -351,30 +366,24 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
         }
         __syncthreads();
         /* the segment's ranges, unrolled whole (a loop back edge would drain the loads in flight):
-         * issue range ch+1 (past the last, range nc-1 again, from L2), then range ch's MFMAs */
+         * range ch's MFMAs (range ch+1 in flight), then range ch+2 issued into its registers (past
+         * the last, range nc-1 again, from L2) */
 #pragma unroll
         for (int ch = 0; ch < SC; ch++) {
             if (ch >= nc)
                 break;
             __builtin_amdgcn_sched_barrier(0);
-            const int nx = ch + 1 < nc ? ch + 1 : nc - 1;
 #pragma unroll
             for (int p = 0; p < KP; p++) {
-                long c = c00 + (long)nx * KP + p;
-                c = c < np ? c : np - 1;
-                q[(ch + 1) & 1][p] = *(const uint4 *)(wq + 64 * c);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int p = 0; p < KP; p++) {
-                const long c = c00 + (long)ch * KP + p;
+                const int c = c00 + ch * KP + p;
                 const bool ok0 = live && c < np, ok1 = live && 2 * c + 1 < nb; /* block 2c, block 2c+1 */
-                const bool keep = lane < 32 ? ok0 : ok1;
                 const uint4 qq = q[ch & 1][p];
-                /* lanes 0-31 hold block 2c, 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
-                const uint32_t a0 = keep ? qq.x : 0u, a1 = keep ? qq.y : 0u, a2 = keep ? qq.z : 0u, a3 = keep ? qq.w : 0u;
-                const auto s02 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
-                const auto s13 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+                /* A block past the matrix (its weights loaded from a clamped index) needs no masking:
+                 * its x limbs in LDS are zero, and a bf16 weight is finite, so its MFMAs give exactly
+                 * 0; its scale is zeroed below, in case the clamped block's scale is not finite.
+                 * Lanes 0-31 hold block 2c, 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
+                const auto s02 = __builtin_amdgcn_permlane32_swap(qq.x, qq.z, false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap(qq.y, qq.w, false, false);
                 const bf16x8 wb[2] = {q8_bf16(s02[0], s13[0]), q8_bf16(s02[1], s13[1])};
                 const int bs = 2 * (ch * KP + p), lr = wave * 16 + n; /* block 2c in the segment, the lane's row in the workgroup */
                 const float d0 = q8_half(dls[lr * DP + bs]), d1 = q8_half(dls[lr * DP + bs + 1]);
@@ -388,6 +397,16 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
 #pragma unroll
                     for (int j = 0; j < 4; j++)
                         acc[j] = __builtin_fmaf(pr[j], d[h], acc[j]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (ch + 2 < SC) {
+                const int nx = ch + 2 < nc ? ch + 2 : nc - 1;
+#pragma unroll
+                for (int p = 0; p < KP; p++) {
+                    int c = c00 + nx * KP + p;
+                    c = c < np ? c : np - 1;
+                    q[ch & 1][p] = *(const uint4 *)(wt + 64L * c + woff);
                 }
             }
         }
