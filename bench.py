@@ -23,9 +23,11 @@ Also in the line, each measured with its own weights rotated through >= 512 MB s
 256 MB Infinity Cache cannot serve them: the single 4096x4096 GEMV, the draft head (first 32768
 rows), the prompt GEMM at M = 16, 40 and 64, the verify path at M = 2..4 (fused pair + down,
 heavy-tailed scales), the 2B layer set, the DeltaNet quartet as four launches and as one round,
-a 9B layer with its norm and residual epilogues, the host-pointer entry points (PCIe-inclusive),
-the whole 9B token through them, and the GGUF load of one 9B layer. Each of these runs in a process
-of its own before the token, on fresh device memory as the token's weights are.
+a 9B layer with its norm and residual epilogues, the host-pointer entry points and the whole 9B
+token through them (PCIe-inclusive, timed from C by intel-phi-apl_amd/q8_hostbench), and the GGUF
+load of one 9B layer. Each of these runs in a process of its own before the token, on fresh device
+memory as the token's weights are. Beside the token: the floor token, the same 129 positions as
+pure reads on the products' own grids (rt_q8_read_dev), one graph.
 """
 import argparse
 import ctypes as c
@@ -204,7 +206,6 @@ def token_trace(b):
 
 def decode_9b(b, steps, warmup):
     layers, head, token, per_token = token_9b(b)
-    b.layers_9b, b.head_9b = layers, head  # the host-pointer token reuses them
     b.lib.rt_graph_begin(b.R)
     token()
     graph = b.lib.rt_graph_end(b.R)
@@ -392,94 +393,22 @@ def deltanet_round(b):
     return out
 
 
-def host_pointers(b):
-    """The reference's entry points with host arrays (x staged in pinned memory and copied to HBM by a
-    kernel, y stored by the product into pinned memory, one wait a call):
-    rt_gemv on 4096x4096 and the 9B DeltaNet quartet queued with rt_gemv_q and run by rt_gemv_go,
-    over rotated weights. The PCIe-inclusive rate, reported beside the HBM-resident one."""
-    out = {}
-    x = np.random.default_rng(3).standard_normal(HIDDEN, dtype=np.float32)
-    ws = rotation(b, 4096, 4096)
-    y = np.empty(4096, np.float32)
-    b.rt.gemv(ws[0], 4096, 4096, x, y)
-    t0 = time.perf_counter()
-    reps = 5
-    for _ in range(reps):
-        for w in ws:
-            b.rt.gemv(w, 4096, 4096, x, y)
-    us = (time.perf_counter() - t0) / (reps * len(ws)) * 1e6
-    out["rt_gemv_4096x4096"] = {"us_per_call": round(us, 2), "GB/s": round(alg_bytes(4096, 4096, 1) / us / 1e3, 1)}
-    for w in ws:
-        b.rt.free(w)
-    shapes = [8192, 4096, 32, 32]
-    quartets = [[b.matrix(r, HIDDEN) for r in shapes] for _ in range(12)]
-    ys = [np.empty(r, np.float32) for r in shapes]
-    per = sum(alg_bytes(r, HIDDEN, 1) for r in shapes) - 3 * 4 * HIDDEN
-
-    def round_(Q):
-        b.rt.gemv_open()
-        for w, r, yy in zip(Q, shapes, ys):
-            b.rt.gemv_q(w, r, HIDDEN, x, yy)
-        b.rt.gemv_go()
-    round_(quartets[0])
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        for Q in quartets:
-            round_(Q)
-    us = (time.perf_counter() - t0) / (reps * len(quartets)) * 1e6
-    out["quartet_round_9b"] = {"us_per_round": round(us, 2), "GB/s": round(per / us / 1e3, 1)}
-    for Q in quartets:
-        for w in Q:
-            b.rt.free(w)
-    return out
+HOSTBENCH = os.path.join(ROOT, "intel-phi-apl_amd", "q8_hostbench")
 
 
-def host_pointer_token(b):
-    """The 9B decode token through the reference's own entry points with host arrays, as its generated
-    code calls them (src/card/rt.h:61-72): per layer rt_gemv (QKV), rt_gemv (out, on QKV's first 4096
-    outputs), rt_gemv_q x 2 + rt_gemv_go (gate and up sharing x, one round), rt_gemv (down, on the
-    gate's outputs: SiLU(g)*u is the caller's host work between the products and is not timed here),
-    each x the previous y in host memory; then rt_gemv (head). The PCIe- and wait-inclusive rate of
-    the same 129 products and 7.23 GB the graph token streams."""
-    layers, head = getattr(b, "layers_9b", None), getattr(b, "head_9b", None)
-    own = layers is None
-    if own:
-        layers = [dict(qkv=b.matrix(QKV, HIDDEN), out=b.matrix(HIDDEN, HIDDEN), gate=b.matrix(FFN, HIDDEN), up=b.matrix(FFN, HIDDEN),
-                       down=b.matrix(HIDDEN, FFN)) for _ in range(LAYERS)]
-        head = b.matrix(VOCAB, HIDDEN)
-    rt = b.rt
-    x0 = np.random.default_rng(4).standard_normal(HIDDEN, dtype=np.float32)
-    yq, yo, yd = np.empty(QKV, np.float32), np.empty(HIDDEN, np.float32), np.empty(HIDDEN, np.float32)
-    g, u, logits = np.empty(FFN, np.float32), np.empty(FFN, np.float32), np.empty(VOCAB, np.float32)
-
-    def token():
-        x = x0
-        for L in layers:
-            rt.gemv(L["qkv"], QKV, HIDDEN, x, yq)
-            rt.gemv(L["out"], HIDDEN, HIDDEN, yq[:HIDDEN], yo)
-            rt.gemv_open()
-            rt.gemv_q(L["gate"], FFN, HIDDEN, yo, g)
-            rt.gemv_q(L["up"], FFN, HIDDEN, yo, u)
-            rt.gemv_go()
-            rt.gemv(L["down"], HIDDEN, FFN, g, yd)
-            x = yd
-        rt.gemv(head, VOCAB, HIDDEN, x, logits)
-
-    token()
-    reps = 5
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        token()
-    ms = (time.perf_counter() - t0) / reps * 1e3
-    per = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + 2 * alg_bytes(FFN, HIDDEN, 1) - 4 * HIDDEN +
-                    alg_bytes(HIDDEN, FFN, 1)) + alg_bytes(VOCAB, HIDDEN, 1)
-    if own:
-        for L in layers:
-            for w in L.values():
-                rt.free(w)
-        rt.free(head)
-    return {"ms_per_token": round(ms, 3), "GB/s": round(per / ms / 1e6, 1), "pct_hbm": round(100 * per / ms / 1e6 / HBM_PEAK_GBS, 1),
-            "calls_per_token": 4 * LAYERS + 1, "bytes_per_token": per, "tokens_timed": reps}
+def host_path():
+    """The host-pointer entry points the reference's generated code calls (src/card/rt.h:61-72),
+    timed from C by intel-phi-apl_amd/q8_hostbench (built by the library's Makefile), in a process
+    of its own started before this one touches the GPU: rt_gemv on 4096x4096 (microseconds a call),
+    the 9B DeltaNet quartet as rt_gemv_q x 4 + rt_gemv_go, and the whole 9B token through rt_gemv /
+    rt_gemv_q + rt_gemv_go (milliseconds a token), each with the calls' phases (x staged, launches,
+    wait, y copied out; rt_host_timing). x and y in host memory: the PCIe- and wait-inclusive rate."""
+    if not os.path.exists(HOSTBENCH):
+        raise SystemExit(f"bench.py: {HOSTBENCH} is not built: run make -C intel-phi-apl_amd")
+    p = subprocess.run([HOSTBENCH, "10"], stdout=subprocess.PIPE, text=True, timeout=600)
+    if p.returncode != 0:
+        raise SystemExit(f"bench.py: {HOSTBENCH} failed (exit {p.returncode})")
+    return json.loads(p.stdout.strip().splitlines()[-1])
 
 
 def epilogues_9b(b):
@@ -1132,7 +1061,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", metavar="SECTIONS", help="comma-separated sections to run instead of the full line (gemv_4096x4096, "
-                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, host_pointer_token_9b, gguf_load_9b_layer, "
+                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, gguf_load_9b_layer, "
                     "epilogues_9b); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
@@ -1160,14 +1089,18 @@ def main():
               "shard by whole 16-row groups, each GPU computing its slice of y)", file=sys.stderr)
         sys.exit(2)
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
-                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("host_pointers", host_pointers),
-                ("host_pointer_token_9b", host_pointer_token),
+                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round),
                 ("gguf_load_9b_layer", gguf_load), ("epilogues_9b", epilogues_9b))
     if a.only:
         sections = sections + (("token_trace", token_trace),)
+        want = a.only.split(",")
+        if "host_pointers" in want:  # the C harness, before this process touches the GPU
+            print(json.dumps({"host_pointers": host_path()}), flush=True)
+            want = [k for k in want if k != "host_pointers"]
+            if not want:
+                return
         q8rt = package()
         b = Bench(q8rt)
-        want = a.only.split(",")
         for key, fn in sections:
             if key in want:
                 print(json.dumps({key: fn(b)}), flush=True)
@@ -1176,6 +1109,9 @@ def main():
     extra = {}
     if not a.no_extra:
         extra = fresh_sections([key for key, _ in sections])
+        log("host_pointers (the C harness) ...")
+        extra["host_pointers"] = host_path()
+        log(f"  {json.dumps(extra['host_pointers'])}")
     q8rt = package()
     b = Bench(q8rt)
     name, cus = b.rt.device_info()

@@ -274,6 +274,20 @@ float rt_timer_stop(struct rt *R);
 void rt_ktime(struct rt *R, int on);
 long rt_ktime_read(struct rt *R, int *kind, long *rows, long *cols, long *t, float *us, char *names, long *grid, long max);
 
+/* The host-pointer calls' own time, for the benchmark (an addition): while on, every call that
+ * waits for its y (rt_gemv, rt_gemm, rt_gemv_go, rt_q8_row's wait excepted) adds, in microseconds of
+ * host time, its phases to us[]: RT_HT_STAGE x into the pinned staging, RT_HT_LAUNCH the launches
+ * (x's copy, the products, the completion flag), RT_HT_WAIT until the flag is seen, RT_HT_COPY_OUT
+ * y out of the pinned staging; rt_host_timing_read returns the number of calls summed.
+ * rt_host_timing(R, on) also clears the sums. */
+#define RT_HT_STAGE 0
+#define RT_HT_LAUNCH 1
+#define RT_HT_WAIT 2
+#define RT_HT_COPY_OUT 3
+#define RT_HT_PHASES 4
+void rt_host_timing(struct rt *R, int on);
+long rt_host_timing_read(struct rt *R, double *us);
+
 /* The device's name and its count of compute units, for reports. */
 void rt_device_info(struct rt *R, char *name, long name_len, int *cus);
 

@@ -75,6 +75,8 @@ _SIGS = {
     "rt_graph_launch": (None, [_vp, _vp]),
     "rt_graph_free": (None, [_vp, _vp]),
     "rt_ktime": (None, [_vp, _int]),
+    "rt_host_timing": (None, [_vp, _int]),
+    "rt_host_timing_read": (_long, [_vp, _vp]),
     "rt_ktime_read": (_long, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _long]),
     "rt_q8_upload_fd": (_vp, [_vp, _int, _u64, _long, _long]),
     "rt_rmsnorm_dev": (None, [_vp, _vp, _long, _long, _long, _vp, _c.c_float, _vp]),

@@ -128,6 +128,11 @@ struct ctx {
     uint8_t *up_host[2] = {nullptr, nullptr}, *up_dev[2] = {nullptr, nullptr};
     hipEvent_t up_done[2] = {nullptr, nullptr};
     size_t up_cap = 0;
+    /* the host-pointer calls' phases (rt_host_timing): microseconds summed over the calls */
+    int htime_on = 0;
+    double ht[RT_HT_PHASES] = {};
+    double ht_t2 = 0.0; /* the current call's end of launching: wait_done sets it */
+    long hcalls = 0;
     /* kernel timing (rt_ktime): one event pair per recorded product */
     int ktime_on = 0;
     std::vector<hipEvent_t> kt_events;
@@ -140,6 +145,12 @@ constexpr size_t KT_MAX = 16384;
  * (src/card/rt.h:85) and uses the last of them. */
 std::vector<ctx *> live;
 ctx *current = nullptr;
+
+/* the host's clock, for the host-pointer calls' phases */
+double now_us()
+{
+    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
 
 ctx *get(struct rt *R, const char *fn)
 {
@@ -440,6 +451,8 @@ void wait_done(ctx *c, const char *what)
     const unsigned seq = ++c->flag_seq;
     q8_launch_flag((q8_stream_t)c->stream, c->flag, seq);
     launched("the completion flag");
+    if (c->htime_on)
+        c->ht_t2 = now_us();
     unsigned long polls = 0;
     q8_wait_until(
         [&] {
@@ -465,6 +478,7 @@ void wait_done(ctx *c, const char *what)
  * 4096x4096, 12288x4096 and 151936x4096 GEMVs, 152 against 25 us at 4096x4096 with 4 tokens. */
 void run_round(ctx *c, job *jobs, int n, const char *what)
 {
+    const double t0 = c->htime_on ? now_us() : 0.0;
     size_t nx = 0, ny = 0;
     for (int i = 0; i < n; i++) {
         job &j = jobs[i];
@@ -492,6 +506,7 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
         if (first)
             memcpy(c->hx + j.x_off, j.x, sizeof(float) * (size_t)(j.t * j.cols));
     }
+    const double t1 = c->htime_on ? now_us() : 0.0;
     q8_launch_copy((q8_stream_t)c->stream, c->dx, c->hx, (long)(nx / 4)); /* nx is a multiple of 64 floats */
     launched("the copy of x");
     /* decode products that share x (and t): one launch for the group */
@@ -517,8 +532,17 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
             product(c, j.w, nullptr, j.rows, j.cols, c->dx + j.x_off, j.cols, j.t, c->hy + j.y_off);
     }
     wait_done(c, what);
+    const double t3 = c->htime_on ? now_us() : 0.0;
     for (int i = 0; i < n; i++)
         memcpy(jobs[i].y, c->hy + jobs[i].y_off, sizeof(float) * (size_t)(jobs[i].t * jobs[i].rows));
+    if (c->htime_on) {
+        const double t4 = now_us();
+        c->ht[RT_HT_STAGE] += t1 - t0;
+        c->ht[RT_HT_LAUNCH] += c->ht_t2 - t1;
+        c->ht[RT_HT_WAIT] += t3 - c->ht_t2;
+        c->ht[RT_HT_COPY_OUT] += t4 - t3;
+        c->hcalls++;
+    }
 }
 
 } // namespace
@@ -1237,6 +1261,25 @@ void rt_graph_free(struct rt *R, void *graph)
     ctx *c = get(R, "rt_graph_free");
     sync_stream(c, "rt_graph_free");
     HIPCHECK(hipGraphExecDestroy((hipGraphExec_t)graph));
+}
+
+void rt_host_timing(struct rt *R, int on)
+{
+    ctx *c = get(R, "rt_host_timing");
+    c->htime_on = on != 0;
+    for (double &v : c->ht)
+        v = 0.0;
+    c->hcalls = 0;
+}
+
+long rt_host_timing_read(struct rt *R, double *us)
+{
+    ctx *c = get(R, "rt_host_timing_read");
+    if (!us)
+        fail("rt_host_timing_read", "us is NULL");
+    for (int k = 0; k < RT_HT_PHASES; k++)
+        us[k] = c->ht[k];
+    return c->hcalls;
 }
 
 void rt_ktime(struct rt *R, int on)
