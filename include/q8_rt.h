@@ -78,8 +78,9 @@ void rt_fini(struct rt *R);
 
 /* ---- products (src/card/rt.h:61-72; rt.c:205-285) */
 
-/* y = W x. x, y host memory: x is copied to HBM, the product runs and stores y into pinned host
- * memory, y is copied out; returns when y is valid. (rt.c:205-214) */
+/* y = W x. x, y host memory: x is staged in pinned host memory (the decode kernels read it there;
+ * the matrix-core and reference-order products get a copy in HBM), the product stores y into
+ * pinned host memory, y is copied out; returns when y is valid. (rt.c:205-214) */
 void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
 
 /* Adjacent products: queue up to RT_BATCH, none reading another's result; rt_gemv_go runs them
@@ -246,11 +247,14 @@ int rt_set_exact(struct rt *R, int exact);
 /* Measurement and test settings (additions), each returning the previous value where it has one:
  * rt_set_epi_apart(R, 1) runs every epilogue as a kernel of its own (the norm's sum then in that
  * kernel's order: an ulp or so of its scale; the residual the same bits); rt_set_upload_chunk sets
- * the upload's chunk in bytes (whole 16-row groups; the bits do not change); rt_gemm_force makes
+ * the upload's chunk in bytes (whole 16-row groups; the bits do not change); rt_set_x_direct(R, 0)
+ * makes the host-pointer calls copy x to HBM before their decode products instead of letting the
+ * kernels read it from pinned host memory (the default, 1; the same bits); rt_gemm_force makes
  * the matrix-core product use `ks` K splits (0: the planner's; other splits, other bits) and, with
  * streaming != 0, the streaming kernel for one token tile instead of the x-resident one (the same
  * sums). */
 int rt_set_epi_apart(struct rt *R, int apart);
+int rt_set_x_direct(struct rt *R, int direct);
 long rt_set_upload_chunk(struct rt *R, long bytes);
 void rt_gemm_force(struct rt *R, int streaming, int ks);
 

@@ -65,6 +65,7 @@ _SIGS = {
     "rt_prims_dev": (None, [_vp, _vp, _vp, _vp, _vp, _long, _vp, _vp, _vp, _vp, _long]),
     "rt_set_exact": (_int, [_vp, _int]),
     "rt_set_epi_apart": (_int, [_vp, _int]),
+    "rt_set_x_direct": (_int, [_vp, _int]),
     "rt_set_upload_chunk": (_long, [_vp, _long]),
     "rt_gemm_force": (None, [_vp, _int, _int]),
     "rt_timer_start": (None, [_vp]),
@@ -207,6 +208,9 @@ class Runtime:
 
     def set_epi_apart(self, on):
         return self.lib.rt_set_epi_apart(self.R, 1 if on else 0)
+
+    def set_x_direct(self, on):
+        return self.lib.rt_set_x_direct(self.R, 1 if on else 0)
 
     def set_upload_chunk(self, nbytes):
         return self.lib.rt_set_upload_chunk(self.R, int(nbytes))

@@ -98,6 +98,7 @@ struct ctx {
     double wait_s = Q8_WAIT_DEFAULT_S; /* Q8_WAIT_S: every host wait's deadline */
     size_t upload_chunk = (size_t)64 << 20; /* Q8_UPLOAD_CHUNK, rt_set_upload_chunk */
     q8_gemm_opts gemm_opts = {0, 0};        /* rt_gemm_force */
+    int x_direct = 1;       /* rt_set_x_direct */
     /* staging for the host-pointer products, in floats: pinned x and y, x's copy in HBM */
     float *hx = nullptr, *hy = nullptr, *dx = nullptr;
     size_t x_cap = 0, y_cap = 0;
@@ -471,11 +472,16 @@ void wait_done(ctx *c, const char *what)
 }
 
 /* A round over host pointers: distinct x staged once, every product (those sharing x as one
- * launch), one wait. x goes to pinned memory on the host and from there to HBM by a copy kernel
- * (one read over the host link, then every workgroup reads HBM); the products store y straight
- * into pinned host memory, which the host reads after the wait. Asynchronous copies in both
- * directions cost more: 19.2 / 32.9 / 148.7 us against 17.6 / 24.3 / 126.6 us a call for the
- * 4096x4096, 12288x4096 and 151936x4096 GEMVs, 152 against 25 us at 4096x4096 with 4 tokens. */
+ * launch), one wait. x goes to pinned memory on the host. When every product of the round is a
+ * decode product (t <= 4, not exact) the kernels read x there directly (rt_set_x_direct, the
+ * default: each workgroup reads all of x, and the L2 serves all but the first read of a line);
+ * otherwise a copy kernel moves it to HBM first. One launch fewer a call: 14.1 against 15.6 us
+ * for a 4096x4096 rt_gemv, 2.82 against 2.92 ms for the 9B token's 129 calls (one run each, from
+ * C); the kernel itself waits ~1.7 us longer for x over the host link. The products store y
+ * straight into pinned host memory, which the host reads after the wait. Asynchronous copies in
+ * both directions cost more: 19.2 / 32.9 / 148.7 us against 17.6 / 24.3 / 126.6 us a call for
+ * the 4096x4096, 12288x4096 and 151936x4096 GEMVs, 152 against 25 us at 4096x4096 with 4 tokens
+ * (against the copy kernel). */
 void run_round(ctx *c, job *jobs, int n, const char *what)
 {
     const double t0 = c->htime_on ? now_us() : 0.0;
@@ -507,8 +513,16 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
             memcpy(c->hx + j.x_off, j.x, sizeof(float) * (size_t)(j.t * j.cols));
     }
     const double t1 = c->htime_on ? now_us() : 0.0;
-    q8_launch_copy((q8_stream_t)c->stream, c->dx, c->hx, (long)(nx / 4)); /* nx is a multiple of 64 floats */
-    launched("the copy of x");
+    bool direct = c->x_direct && !c->exact;
+    for (int i = 0; i < n; i++)
+        direct = direct && jobs[i].t <= 4;
+    const float *xb = c->dx;
+    if (direct) {
+        xb = c->hx;
+    } else {
+        q8_launch_copy((q8_stream_t)c->stream, c->dx, c->hx, (long)(nx / 4)); /* nx is a multiple of 64 floats */
+        launched("the copy of x");
+    }
     /* decode products that share x (and t): one launch for the group */
     bool done[RT_BATCH] = {};
     for (int i = 0; i < n && !c->exact; i++) {
@@ -522,14 +536,14 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
             if (!done[j] && jobs[j].x_off == jobs[i].x_off && jobs[j].t == jobs[i].t && jobs[j].cols == jobs[i].cols) {
                 w[k] = jobs[j].w, rows[k] = jobs[j].rows, y[k] = c->hy + jobs[j].y_off, idx[k++] = j;
             }
-        if (k > 1 && round_launch(c, k, w, rows, jobs[i].cols, c->dx + jobs[i].x_off, jobs[i].cols, jobs[i].t, y))
+        if (k > 1 && round_launch(c, k, w, rows, jobs[i].cols, xb + jobs[i].x_off, jobs[i].cols, jobs[i].t, y))
             for (int j = 0; j < k; j++)
                 done[idx[j]] = true;
     }
     for (int i = 0; i < n; i++) {
         const job &j = jobs[i];
         if (!done[i])
-            product(c, j.w, nullptr, j.rows, j.cols, c->dx + j.x_off, j.cols, j.t, c->hy + j.y_off);
+            product(c, j.w, nullptr, j.rows, j.cols, xb + j.x_off, j.cols, j.t, c->hy + j.y_off);
     }
     wait_done(c, what);
     const double t3 = c->htime_on ? now_us() : 0.0;
@@ -1204,6 +1218,14 @@ long rt_set_upload_chunk(struct rt *R, long bytes)
         fail("rt_set_upload_chunk", "bytes must be positive");
     const long old = (long)c->upload_chunk;
     c->upload_chunk = (size_t)bytes;
+    return old;
+}
+
+int rt_set_x_direct(struct rt *R, int direct)
+{
+    ctx *c = get(R, "rt_set_x_direct");
+    const int old = c->x_direct;
+    c->x_direct = direct != 0;
     return old;
 }
 

@@ -460,14 +460,17 @@ def test_deterministic_and_prefix(rt):
     assert np.array_equal(p.view(np.uint32), a[:, :1024].view(np.uint32))
 
 
-def test_host_pointer_entry_points(rt):
+@pytest.mark.parametrize("direct", [False, True], ids=["x_copied", "x_direct"])
+def test_host_pointer_entry_points(rt, direct):
     """rt_gemv, rt_gemm and a queued round of 4 products sharing x (open/go) give the same bits as the
-    device entry points."""
+    device entry points, with x copied to HBM first or read by the decode kernels from the pinned
+    staging (rt_set_x_direct)."""
     rows, cols = 2048, 2048
     rng = np.random.default_rng(31)
     mats = [synth.q8_rows(rng, rows, cols) for _ in range(4)]
     x = synth.x_f32(rng, 6, cols)
     ws = [rt.upload(m, rows, cols) for m in mats]
+    old_direct = rt.set_x_direct(direct)
     try:
         want1 = [gpu_gemm(rt, m, rows, cols, x[0], w=w)[0] for m, w in zip(mats, ws)]
         y = np.empty(rows, np.float32)
@@ -494,16 +497,26 @@ def test_host_pointer_entry_points(rt):
         assert np.array_equal(ys[1].view(np.uint32), want1[0].view(np.uint32))
         assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, mats[3], rows, cols, x, w=ws[3]).view(np.uint32))
     finally:
+        rt.set_x_direct(old_direct)
         for w in ws:
             rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
-def test_host_pointer_staging_grows_and_refreshes(rt):
+@pytest.mark.parametrize("direct", [False, True], ids=["x_copied", "x_direct"])
+def test_host_pointer_staging_grows_and_refreshes(rt, direct):
     """The host-pointer products store y into pinned staging that grows with the call: a sequence of
     growing shapes and token counts (up to 70 tokens, two matrix-core launches into one y), the
     reference-order kernel, and a repeat with a new x, each equal bit for bit to the device path."""
     rng = np.random.default_rng(41)
-    cases = [(256, 1024, 1), (4096, 1024, 3), (1024, 4096, 16), (8192, 1024, 70), (512, 2048, 4)]
+    cases = [(256, 1024, 1), (4096, 1024, 3), (1024, 4096, 16), (8192, 1024, 70), (512, 2048, 4), (2048, 4096, 1)]
+    old_direct = rt.set_x_direct(direct)
+    try:
+        staging_cases(rt, rng, cases)
+    finally:
+        rt.set_x_direct(old_direct)
+
+
+def staging_cases(rt, rng, cases):
     for rows, cols, t in cases:
         q8 = synth.q8_rows(rng, rows, cols)
         w = rt.upload(q8, rows, cols)
@@ -511,7 +524,7 @@ def test_host_pointer_staging_grows_and_refreshes(rt):
             for exact in (False, True) if t <= 4 else (False,):
                 old = rt.set_exact(exact)
                 try:
-                    for rep in range(2):
+                    for rep in range(3):
                         x = synth.x_f32(rng, t, cols)
                         Y = np.full((t, rows), np.nan, np.float32)
                         if t == 1:
