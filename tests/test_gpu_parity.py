@@ -460,17 +460,29 @@ def test_deterministic_and_prefix(rt):
     assert np.array_equal(p.view(np.uint32), a[:, :1024].view(np.uint32))
 
 
-@pytest.mark.parametrize("direct", [False, True], ids=["x_copied", "x_direct"])
-def test_host_pointer_entry_points(rt, direct):
+HOST_MODES = {"x_copied": False, "x_direct": True}
+
+
+def host_mode(rt, mode):
+    """Sets how the host-pointer calls stage x (rt_set_x_direct); returns the previous setting."""
+    return rt.set_x_direct(HOST_MODES[mode])
+
+
+def restore_host_mode(rt, old):
+    rt.set_x_direct(old)
+
+
+@pytest.mark.parametrize("mode", list(HOST_MODES))
+def test_host_pointer_entry_points(rt, mode):
     """rt_gemv, rt_gemm and a queued round of 4 products sharing x (open/go) give the same bits as the
     device entry points, with x copied to HBM first or read by the decode kernels from the pinned
-    staging (rt_set_x_direct)."""
+    staging."""
     rows, cols = 2048, 2048
     rng = np.random.default_rng(31)
     mats = [synth.q8_rows(rng, rows, cols) for _ in range(4)]
     x = synth.x_f32(rng, 6, cols)
     ws = [rt.upload(m, rows, cols) for m in mats]
-    old_direct = rt.set_x_direct(direct)
+    old_mode = host_mode(rt, mode)
     try:
         want1 = [gpu_gemm(rt, m, rows, cols, x[0], w=w)[0] for m, w in zip(mats, ws)]
         y = np.empty(rows, np.float32)
@@ -497,23 +509,51 @@ def test_host_pointer_entry_points(rt, direct):
         assert np.array_equal(ys[1].view(np.uint32), want1[0].view(np.uint32))
         assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, mats[3], rows, cols, x, w=ws[3]).view(np.uint32))
     finally:
-        rt.set_x_direct(old_direct)
+        restore_host_mode(rt, old_mode)
         for w in ws:
             rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
-@pytest.mark.parametrize("direct", [False, True], ids=["x_copied", "x_direct"])
-def test_host_pointer_staging_grows_and_refreshes(rt, direct):
+@pytest.mark.parametrize("mode", list(HOST_MODES))
+def test_host_call_waits_for_stream_work(rt, mode):
+    """A host-pointer call made while the runtime's stream still repacks the matrix it reads (no
+    wait between the two) sees the repacked matrix and not the fill before it."""
+    rows, cols = 8192, 4096
+    rng = np.random.default_rng(37)
+    q8 = synth.q8_rows(rng, rows, cols)
+    x = synth.x_f32(rng, 2, cols)
+    src, out = rt.alloc(q8.nbytes), rt.alloc(q8.nbytes)
+    old_mode = host_mode(rt, mode)
+    try:
+        rt.to_dev(src, q8)
+        rt.lib.rt_f32_fill_dev(rt.R, c.c_void_p(out), q8.nbytes // 4, 99)
+        rt.sync()
+        for rep in range(3):
+            rt.lib.rt_q8_repack_dev(rt.R, c.c_void_p(src), rows, cols, c.c_void_p(out))
+            y = np.full(rows, np.nan, np.float32)
+            rt.gemv(out, rows, cols, x[rep % 2], y)
+            say("host call after queued repack", mode, rep)
+            want = gpu_gemm(rt, q8, rows, cols, x[rep % 2:rep % 2 + 1])[0]
+            assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+            rt.lib.rt_f32_fill_dev(rt.R, c.c_void_p(out), q8.nbytes // 4, 100 + rep)
+    finally:
+        restore_host_mode(rt, old_mode)
+        rt.free(out)  # and with it the handle rt_q8_repack_dev registered there
+        rt.free(src)
+
+
+@pytest.mark.parametrize("mode", list(HOST_MODES))
+def test_host_pointer_staging_grows_and_refreshes(rt, mode):
     """The host-pointer products store y into pinned staging that grows with the call: a sequence of
     growing shapes and token counts (up to 70 tokens, two matrix-core launches into one y), the
     reference-order kernel, and a repeat with a new x, each equal bit for bit to the device path."""
     rng = np.random.default_rng(41)
     cases = [(256, 1024, 1), (4096, 1024, 3), (1024, 4096, 16), (8192, 1024, 70), (512, 2048, 4), (2048, 4096, 1)]
-    old_direct = rt.set_x_direct(direct)
+    old_mode = host_mode(rt, mode)
     try:
         staging_cases(rt, rng, cases)
     finally:
-        rt.set_x_direct(old_direct)
+        restore_host_mode(rt, old_mode)
 
 
 def staging_cases(rt, rng, cases):
