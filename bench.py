@@ -733,16 +733,16 @@ GEMM_PROFILE_CMDS = [
     "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/gprof_fetch -o run -- python3 bench.py --only prompt_gemm",
     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv "
     "-d gpurun_out/gprof_mfma -o run -- python3 bench.py --only prompt_gemm",
-    "rocprofv3 --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_VALU SQ_INSTS_VMEM_RD "
-    "SQ_INSTS_VALU GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/gprof_sq -o run -- python3 bench.py --only prompt_gemm,draft_head "
+    "rocprofv3 --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_INSTS_VMEM_RD SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
+    "GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/gprof_sq -o run -- python3 bench.py --only prompt_gemm,draft_head "
     "> gpurun_out/gprof_sq.log 2>&1",
     "rocprofv3 --pmc TA_TA_BUSY_sum TA_ADDR_STALLED_BY_TC_CYCLES_sum TD_TD_BUSY_sum TD_TC_STALL_sum TCP_TCP_TA_DATA_STALL_CYCLES_sum "
     "TCP_PENDING_STALL_CYCLES_sum TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum GRBM_GUI_ACTIVE --output-format csv "
     "-d gpurun_out/gprof_ta -o run -- python3 bench.py --only prompt_gemm,draft_head",
     "python3 bench.py --summarize-gemm gpurun_out",
 ]
-GEMM_STALL_COUNTERS = ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_VALU",
-                       "SQ_INSTS_VMEM_RD", "SQ_INSTS_VALU", "TA_TA_BUSY_sum", "TA_ADDR_STALLED_BY_TC_CYCLES_sum", "TD_TD_BUSY_sum",
+GEMM_STALL_COUNTERS = ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VMEM_RD", "SQ_INSTS_VALU",
+                       "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "TA_TA_BUSY_sum", "TA_ADDR_STALLED_BY_TC_CYCLES_sum", "TD_TD_BUSY_sum",
                        "TD_TC_STALL_sum", "TCP_TCP_TA_DATA_STALL_CYCLES_sum", "TCP_PENDING_STALL_CYCLES_sum", "TCP_TCC_READ_REQ_LATENCY_sum",
                        "TCP_TCC_READ_REQ_sum")
 
@@ -813,11 +813,14 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
         text += ["## Where the waves wait (two more counter passes)", "",
                  f"Per kernel and grid, the kernel's cycles K = GRBM_GUI_ACTIVE / {xcds} of the same pass; a CU's TA, TD and TCP "
                  f"count each on their own (256 of each; their _sum over the device / (256 x K) is the share of a unit's cycles); "
-                 f"SQ_WAVE_CYCLES and SQ_WAIT_INST_ANY are in quad-cycles (x 4). The draft head's decode kernel (1 KiB of one row "
-                 "a load instruction, every load of a wave issued at once) streams at 78 % of HBM: the contrast.", "",
-                 "| Product | Kernel | Waves a SIMD | Wave cycles waiting % | VMEM issue % | VALU issue % | TA busy % | TA stalled by TCP % | "
+                 f"SQ_WAVE_CYCLES and SQ_WAIT_INST_ANY are in quad-cycles (x 4). VALU busy % is an estimate from instruction "
+                 f"counts: (SQ_INSTS_VALU - SQ_INSTS_MFMA) x 4 cycles (a wave64 instruction on a 16-lane SIMD) over K x {simds} "
+                 "SIMDs. The draft head's decode kernel (1 KiB of one row a load instruction, every load of a wave issued at "
+                 "once) streams at 78 % of HBM: the contrast.", "",
+                 "| Product | Kernel | Waves a SIMD | Wave cycles waiting % | VALU busy % (est.) | TA busy % | TA stalled by TCP % | "
                  "TD stalled by TCP % | TCP stalled on TA data % | TCP pending % | L2 read latency cycles | Loads a wave | "
-                 "VALU instructions a wave |", "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+                 "VALU instructions a wave | MFMA instructions a wave | LDS instructions a wave |",
+                 "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
         for shape, key in keyed:
             st = stall.get(key, {})
             g = lambda sub, n: mean(st.get((sub, n), []))  # noqa: E731
@@ -826,13 +829,13 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
             waves = g("gprof_sq", "SQ_WAVES")
             text.append(f"| {shape} | `{key[0]}` | {4 * g('gprof_sq', 'SQ_WAVE_CYCLES') / (ksq * simds):.2f} | "
                         f"{100 * g('gprof_sq', 'SQ_WAIT_INST_ANY') / g('gprof_sq', 'SQ_WAVE_CYCLES'):.1f} | "
-                        f"{100 * g('gprof_sq', 'SQ_ACTIVE_INST_VMEM') / (ksq * simds):.1f} | "
-                        f"{100 * g('gprof_sq', 'SQ_ACTIVE_INST_VALU') / (ksq * simds):.1f} | "
+                        f"{100 * 4 * (g('gprof_sq', 'SQ_INSTS_VALU') - g('gprof_sq', 'SQ_INSTS_MFMA')) / (ksq * simds):.1f} | "
                         f"{100 * g('gprof_ta', 'TA_TA_BUSY_sum') / (cu * kta):.1f} | {100 * g('gprof_ta', 'TA_ADDR_STALLED_BY_TC_CYCLES_sum') / (cu * kta):.1f} | "
                         f"{100 * g('gprof_ta', 'TD_TC_STALL_sum') / (cu * kta):.1f} | {100 * g('gprof_ta', 'TCP_TCP_TA_DATA_STALL_CYCLES_sum') / (cu * kta):.1f} | "
                         f"{100 * g('gprof_ta', 'TCP_PENDING_STALL_CYCLES_sum') / (cu * kta):.1f} | "
                         f"{g('gprof_ta', 'TCP_TCC_READ_REQ_LATENCY_sum') / g('gprof_ta', 'TCP_TCC_READ_REQ_sum'):.0f} | "
-                        f"{g('gprof_sq', 'SQ_INSTS_VMEM_RD') / waves:.1f} | {g('gprof_sq', 'SQ_INSTS_VALU') / waves:.0f} |")
+                        f"{g('gprof_sq', 'SQ_INSTS_VMEM_RD') / waves:.1f} | {g('gprof_sq', 'SQ_INSTS_VALU') / waves:.0f} | "
+                        f"{g('gprof_sq', 'SQ_INSTS_MFMA') / waves:.0f} | {g('gprof_sq', 'SQ_INSTS_LDS') / waves:.0f} |")
         text.append("")
     open(out, "w").write("\n".join(text))
     print(f"wrote {out}")

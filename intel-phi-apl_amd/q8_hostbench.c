@@ -11,7 +11,8 @@
  *                       x), rt_gemv (down 4096x12288), 32 distinct layers, then rt_gemv (head
  *                       151936x4096): milliseconds a token and the phases of its calls.
  * Weights are synthetic (rt_q8_fill_dev, repacked on the device). Needs the GPU. Usage:
- * q8_hostbench [passes [x_direct]] (default 10 passes; x_direct 1: rt_set_x_direct). */
+ * q8_hostbench [passes [x_direct]]: 10 passes by default; x_direct 0 or 1 sets rt_set_x_direct
+ * (default: the library's). */
 #define _POSIX_C_SOURCE 199309L
 #include <stdio.h>
 #include <stdlib.h>
@@ -64,11 +65,14 @@ static void phases(const char *key, double calls_per_unit)
 int main(int argc, char **argv)
 {
     const int passes = argc > 1 ? atoi(argv[1]) : 10;
-    const int direct = argc > 2 ? atoi(argv[2]) : 0;
     if (rt_init(&R, 1) != 0) {
         fprintf(stderr, "q8_hostbench: rt_init failed\n");
         return 1;
     }
+    /* the library's default unless the second argument sets it */
+    int direct = rt_set_x_direct(&R, 1);
+    if (argc > 2)
+        direct = atoi(argv[2]) != 0;
     rt_set_x_direct(&R, direct);
     staging = rt_dev_alloc(&R, 151936L * 4096 / 32 * 34);
     const long H = 4096, F = 12288, Q = 6144, V = 151936;

@@ -94,6 +94,35 @@ def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path):
         assert rows[s][-2] == "10.0", s   # MFMA busy: 1024 cycles over (80 / 8 XCDs x 1024 SIMDs)
 
 
+def test_gemm_stall_table_by_hand(tmp_path):
+    """The GEMM profile's stall table, per kernel and grid, from the SQ pass and the TA/TD/TCP pass,
+    each over its own GRBM_GUI_ACTIVE (summed over 8 XCDs): waves a SIMD and waiting from the
+    quad-cycle counters, the VALU estimate from instruction counts (MFMAs left out, 4 cycles an
+    instruction), the units' shares over 256 CUs, the L2 latency a request, counts a wave."""
+    run = tmp_path / "run"
+    xr = "gemm_xres<2, 16, 8>"
+    line = {"prompt_gemm": {"M16 12288x4096": {"kernel": xr, "grid": 245760, "kernel_us": 18.0, "product_us": 19.0, "GFLOPS": 1.0}}}
+    os.makedirs(run)
+    (run / "gprof_stats.log").write_text(json.dumps(line) + "\n")
+    _trace(str(run / "gprof_stats" / "run_kernel_trace.csv"), [(xr, 245760, [17.0])])
+    _counters(str(run / "gprof_fetch" / "run_counter_collection.csv"), [(xr, 245760, "FETCH_SIZE", [30000.0])])
+    _counters(str(run / "gprof_mfma" / "run_counter_collection.csv"), [(xr, 245760, "GRBM_GUI_ACTIVE", [80.0])])
+    k = 1000.0  # the kernel's cycles
+    sq = {"GRBM_GUI_ACTIVE": 8 * k, "SQ_WAVES": 3840.0, "SQ_WAVE_CYCLES": 1024 * k / 4 * 2.0, "SQ_WAIT_INST_ANY": 1024 * k / 4 * 2.0 * 0.3,
+          "SQ_INSTS_VALU": 1024 * k / 4 * 0.4 + 500.0, "SQ_INSTS_MFMA": 500.0, "SQ_INSTS_LDS": 3840.0 * 7, "SQ_INSTS_VMEM_RD": 3840.0 * 27,
+          "SQ_BUSY_CYCLES": 1.0}
+    ta = {"GRBM_GUI_ACTIVE": 8 * k, "TA_TA_BUSY_sum": 256 * k * 0.32, "TA_ADDR_STALLED_BY_TC_CYCLES_sum": 256 * k * 0.22, "TD_TD_BUSY_sum": 1.0,
+          "TD_TC_STALL_sum": 256 * k * 0.31, "TCP_TCP_TA_DATA_STALL_CYCLES_sum": 256 * k * 0.003, "TCP_PENDING_STALL_CYCLES_sum": 256 * k * 0.09,
+          "TCP_TCC_READ_REQ_LATENCY_sum": 826.0 * 100, "TCP_TCC_READ_REQ_sum": 100.0}
+    _counters(str(run / "gprof_sq" / "run_counter_collection.csv"), [(xr, 245760, n, [v]) for n, v in sq.items()])
+    _counters(str(run / "gprof_ta" / "run_counter_collection.csv"), [(xr, 245760, n, [v]) for n, v in ta.items()])
+    out = tmp_path / "gemm.md"
+    bench.summarize_gemm(str(run), out=str(out))
+    text = out.read_text().split("## Where the waves wait", 1)[1]
+    row = [c.strip() for c in next(l for l in text.splitlines() if l.startswith("| M16")).split("|")[3:-1]]
+    assert row == ["2.00", "30.0", "40.0", "32.0", "22.0", "31.0", "0.3", "9.0", "826", "27.0", "27", "0", "7"]
+
+
 def test_verify_summary_per_kernel_and_grid(tmp_path):
     """bench.summarize_verify: each verify product (M, pair or down) is matched to its own kernel and
     grid; counters per weight and per SIMD cycle as computed by hand (GRBM_GUI_ACTIVE summed over 8
