@@ -543,6 +543,42 @@ def test_host_call_waits_for_stream_work(rt, mode):
 
 
 @pytest.mark.parametrize("mode", list(HOST_MODES))
+def test_host_calls_alternating_x_see_each_new_x(rt, mode):
+    """300 host-pointer calls back to back, x cycling through three vectors (and a round of two
+    products every fourth call): each y equals, bit for bit, the device product of the x that call
+    passed, so no call reads the previous call's x from a cache (the decode kernels read x from
+    the pinned staging that the host rewrites before each call)."""
+    rows, cols = 2048, 4096
+    rng = np.random.default_rng(43)
+    mats = [synth.q8_rows(rng, rows, cols) for _ in range(2)]
+    xs = synth.x_f32(rng, 3, cols)
+    ws = [rt.upload(m, rows, cols) for m in mats]
+    old_mode = host_mode(rt, mode)
+    try:
+        want = [[gpu_gemm(rt, m, rows, cols, xs[k], w=w)[0] for k in range(3)] for m, w in zip(mats, ws)]
+        y0, y1 = np.empty(rows, np.float32), np.empty(rows, np.float32)
+        bad = []
+        for i in range(300):
+            k = i % 3
+            if i % 4 == 3:
+                rt.gemv_q(ws[0], rows, cols, xs[k], y0)
+                rt.gemv_q(ws[1], rows, cols, xs[k], y1)
+                rt.gemv_go()
+                ok = np.array_equal(y0.view(np.uint32), want[0][k].view(np.uint32)) and np.array_equal(y1.view(np.uint32), want[1][k].view(np.uint32))
+            else:
+                rt.gemv(ws[i % 2], rows, cols, xs[k], y0)
+                ok = np.array_equal(y0.view(np.uint32), want[i % 2][k].view(np.uint32))
+            if not ok:
+                bad.append(i)
+        say("alternating x", mode, "calls 300, mismatches", len(bad))
+        assert not bad, bad[:10]
+    finally:
+        restore_host_mode(rt, old_mode)
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
+@pytest.mark.parametrize("mode", list(HOST_MODES))
 def test_host_pointer_staging_grows_and_refreshes(rt, mode):
     """The host-pointer products store y into pinned staging that grows with the call: a sequence of
     growing shapes and token counts (up to 70 tokens, two matrix-core launches into one y), the
