@@ -466,12 +466,14 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
 struct gemm_cfg {
     int mg, rt, kp, nw;
 };
-#define GEMM_CFGS(X) X(1, 1, 2, 16) X(2, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 16)
+/* 16 waves (256 rows) a workgroup, or 12 (192 rows) for the shapes where that leaves fewer compute
+ * units idle (nw_of); the 12-wave instances of one token tile are the streaming twins of the
+ * x-resident kernel's */
+#define GEMM_CFGS(X) X(1, 1, 2, 16) X(2, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 16) X(1, 1, 2, 12) X(3, 1, 2, 12) X(4, 1, 2, 12)
 
-/* the x-resident kernel for one token tile: 2-pair ranges, 16 waves, segments of 8 ranges (x
- * limbs 96 KiB and scales 17 KiB of LDS: one workgroup a CU) */
+/* the x-resident kernel for one token tile: 2-pair ranges, 16 or 12 waves, segments of 8 ranges
+ * (x limbs 96 KiB and scales 13-17 KiB of LDS: one workgroup a CU) */
 #define XRES_KP 2
-#define XRES_NW 16
 #define XRES_SC 8
 
 /* every configuration streams ranges of the same KP pairs, so a K split of cps ranges covers the
@@ -510,13 +512,19 @@ struct gemm_plan {
  * X). As many splits as fill the device with one resident round of the x-resident kernel's
  * workgroups (256 rows each), fewer if the partials of a 64-token launch would not fit the
  * workspace. ks_force > 0 sets the split count instead (a test hook: other splits, other bits). */
-static void split_of(long rows, long cols, int ks_force, int *ks, int *cps)
+/* resident workgroups of the x-resident kernel with nw waves (16 or 12) */
+static long resident_xres(int nw)
 {
-    static long nx = 0;
-    const long tiles = (rows + 16L * XRES_NW - 1) / (16L * XRES_NW);
+    static long n16 = 0, n12 = 0;
+    return nw == 12 ? resident(gemm_xres<XRES_KP, 12, XRES_SC>, 64 * 12, n12) : resident(gemm_xres<XRES_KP, 16, XRES_SC>, 64 * 16, n16);
+}
+
+static void split_of(long rows, long cols, int nw, int ks_force, int *ks, int *cps)
+{
+    const long tiles = (rows + 16L * nw - 1) / (16L * nw);
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
     const long ranges = (np + XRES_KP - 1) / XRES_KP;
-    long split = ks_force > 0 ? ks_force : resident(gemm_xres<XRES_KP, XRES_NW, XRES_SC>, 64 * XRES_NW, nx) / tiles;
+    long split = ks_force > 0 ? ks_force : resident_xres(nw) / tiles;
     split = split < 1 ? 1 : split > ranges ? ranges : split;
     long per = (ranges + split - 1) / split;
     while (per < ranges && (ranges + per - 1) / per * 64 * rows > Q8_GEMM_PART_MAX)
@@ -525,12 +533,37 @@ static void split_of(long rows, long cols, int ks_force, int *ks, int *cps)
     *ks = (int)((ranges + per - 1) / per);
 }
 
+/* The waves a workgroup for a shape, 16 or 12, from the shape alone (so the split, and the bits,
+ * stay independent of t): the one whose grid takes the fewest rounds of resident workgroups times
+ * the rows and ranges a workgroup streams; 16 on a tie. At 12288 x 4096, 16 waves make 48 row
+ * tiles x 5 splits = 240 workgroups of 256 rows x 7 ranges, 16 compute units idle; 12 make 64 x 4
+ * = 256 of 192 rows x 8 ranges. At 4096 x 12288 16 waves fill the device (16 x 16 of 256 x 6). */
+static int nw_of(long rows, long cols, int ks_force)
+{
+    long best = -1;
+    int pick = 16;
+    for (int nw : {16, 12}) {
+        int ks, cps;
+        split_of(rows, cols, nw, ks_force, &ks, &cps);
+        const long tiles = (rows + 16L * nw - 1) / (16L * nw), res = resident_xres(nw);
+        const long cost = (tiles * ks + res - 1) / res * 16L * nw * cps;
+        if (best < 0 || cost < best) {
+            best = cost;
+            pick = nw;
+        }
+    }
+    return pick;
+}
+
 static gemm_plan plan_of(long rows, long cols, long t, q8_gemm_opts o)
 {
     const long mt = ((t < 64 ? t : 64) + 15) / 16;
     static const gemm_cfg CFG[5] = {{0, 0, 0, 0}, {1, 1, 2, 16}, {2, 1, 2, 8}, {3, 1, 2, 16}, {4, 1, 2, 16}};
+    const int nw = nw_of(rows, cols, o.ks);
     gemm_plan p = {CFG[mt], mt == 1 && !o.streaming, 0, 0};
-    split_of(rows, cols, o.ks, &p.ks, &p.cps);
+    if (mt != 2)
+        p.c.nw = nw;
+    split_of(rows, cols, nw, o.ks, &p.ks, &p.cps);
     return p;
 }
 
@@ -560,9 +593,13 @@ void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols
     const float *r1 = ks > 1 ? nullptr : res;
     bool done = false;
     if (p.xres) {
-        const long tiles = (rows + 16L * XRES_NW - 1) / (16L * XRES_NW);
-        Q8_LAUNCH(q8_time_name("gemm_xres", 3, XRES_KP, XRES_NW, XRES_SC), (gemm_xres<XRES_KP, XRES_NW, XRES_SC>), dim3((unsigned)(tiles * ks)),
-                  dim3(64 * XRES_NW), s, (const uint8_t *)w, rows, cols, x, x_stride, t, ks, cps, out, out, r1);
+        const long tiles = (rows + 16L * p.c.nw - 1) / (16L * p.c.nw);
+        if (p.c.nw == 12)
+            Q8_LAUNCH(q8_time_name("gemm_xres", 3, XRES_KP, 12, XRES_SC), (gemm_xres<XRES_KP, 12, XRES_SC>), dim3((unsigned)(tiles * ks)), dim3(64 * 12), s,
+                      (const uint8_t *)w, rows, cols, x, x_stride, t, ks, cps, out, out, r1);
+        else
+            Q8_LAUNCH(q8_time_name("gemm_xres", 3, XRES_KP, 16, XRES_SC), (gemm_xres<XRES_KP, 16, XRES_SC>), dim3((unsigned)(tiles * ks)), dim3(64 * 16), s,
+                      (const uint8_t *)w, rows, cols, x, x_stride, t, ks, cps, out, out, r1);
         done = true;
     }
 #define GO(G, R, P, N)                                                                                                 \
