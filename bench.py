@@ -662,6 +662,65 @@ def _kname(full):
     return n[5:] if n.startswith("void ") else n
 
 
+BUILD = os.path.join(ROOT, "intel-phi-apl_amd", "_build")
+LLVM = "/opt/rocm/llvm/bin"
+
+
+def kernel_registers(objs=("q8_kernels.o", "q8_gemm.o"), arch="gfx950"):
+    """{kernel name as rocprof prints it: (VGPRs, AGPRs, SGPRs, scratch bytes a lane)} from the metadata
+    of the gfx950 code objects in the library's own build (each object's offload bundle unbundled),
+    or {} where the build or the tools are missing. rocprof's kernel trace reports a VGPR count of
+    its own that is half the code object's for these kernels, so the profiles take these."""
+    import re
+    import tempfile
+
+    regs = {}
+    with tempfile.TemporaryDirectory() as d:
+        for obj in objs:
+            fb, co = os.path.join(d, obj + ".fatbin"), os.path.join(d, obj + ".co")
+            try:
+                subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", os.path.join(BUILD, obj), fb], check=True, capture_output=True)
+                subprocess.run([os.path.join(LLVM, "clang-offload-bundler"), "--unbundle", "--type=o", f"--input={fb}",
+                                f"--targets=hipv4-amdgcn-amd-amdhsa--{arch}", f"--output={co}"], check=True, capture_output=True)
+                notes = subprocess.run([os.path.join(LLVM, "llvm-readelf"), "--notes", co], check=True, capture_output=True, text=True).stdout
+            except (OSError, subprocess.CalledProcessError):
+                continue
+            found = []
+            for block in re.split(r"\n  - \.agpr_count", notes)[1:]:
+                field = lambda k: re.search(rf"\.{k}:\s+(\S+)", block)  # noqa: E731
+                if not field("name"):
+                    continue
+                found.append((field("name").group(1), (int(field("vgpr_count").group(1)), int(re.match(r":\s+(\d+)", block).group(1)),
+                                                        int(field("sgpr_count").group(1)), int(field("private_segment_fixed_size").group(1)))))
+            try:
+                names = subprocess.run(["c++filt"], input="\n".join(n for n, _ in found), check=True, capture_output=True, text=True).stdout.split("\n")
+            except (OSError, subprocess.CalledProcessError):
+                continue
+            for (_, r), dn in zip(found, names):
+                regs[_kname(dn)] = r
+    return regs
+
+
+def waves_by_registers(vgprs, agprs):
+    """Waves a SIMD the register file allows (512 a lane, VGPRs and AGPRs each in blocks of 8), at most 8."""
+    used = -(-vgprs // 8) * 8 + -(-agprs // 8) * 8
+    return min(8, 512 // used) if used else 8
+
+
+LDS_BYTES = 160 * 1024
+
+
+def occupancy_cells(regs, name, lds, wg_threads):
+    """'VGPRs | waves a SIMD at most, by registers / by LDS' for a kernel (its registers from the code
+    object, its LDS a workgroup and workgroup size from the kernel trace)."""
+    r = regs.get(name)
+    if not r:
+        return "? | ?"
+    waves_wg = max(1, wg_threads // 64)
+    by_lds = (LDS_BYTES // lds) * waves_wg / 4 if lds else 8
+    return f"{r[0]} | {waves_by_registers(r[0], r[1])} / {min(8, by_lds):g}"
+
+
 def summarize(run_dir, out=DECODE_PROFILE):
     """profiles/gemv_decode_9b_m1.md from the three rocprofv3 runs of PROFILE_CMDS: per product of the
     token, the kernel, its average duration in the kernel trace and in the benchmark's own events,
@@ -756,10 +815,12 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
     from collections import defaultdict
 
     line = json.loads(next(l for l in open(os.path.join(run_dir, "gprof_stats.log")) if l.startswith('{"prompt_gemm"')))["prompt_gemm"]
-    trace = defaultdict(list)
+    trace, wg_shape = defaultdict(list), {}
     for r in csv.DictReader(open(os.path.join(run_dir, "gprof_stats", "run_kernel_trace.csv"))):
         g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
         trace[(_kname(r["Kernel_Name"]), g)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        wg_shape[(_kname(r["Kernel_Name"]), g)] = (int(r.get("LDS_Block_Size") or 0), int(r.get("Workgroup_Size_X") or 64))
+    regs = kernel_registers()
     cnt = defaultdict(lambda: defaultdict(list))
     stall = defaultdict(lambda: defaultdict(list))  # the two stall passes, each with its own GRBM_GUI_ACTIVE
     for sub in ("gprof_fetch", "gprof_mfma", "gprof_sq", "gprof_ta"):
@@ -789,19 +850,22 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
         tr = trace.get(key, [])
         rows.append(f"| {shape} | `{name}` | {mean(tr):.2f} | {k['kernel_us']:.2f} | {k['product_us']:.2f} | {k['GFLOPS']:.0f} | "
                     f"{2.0 * mean(c.get('FETCH_SIZE', [])) * 1024 / 1e6:.1f} | {alg_bytes(r_, c_, m) / 1e6:.1f} | {100 * util:.1f} | "
-                    f"{mops * 512 / issued:.3f} |")
+                    f"{mops * 512 / issued:.3f} | {occupancy_cells(regs, name, *wg_shape.get(key, (0, 64)))} |")
     text = ["# Prompt / verify GEMM on the matrix cores, 9B FFN shapes (rocprofv3)", "",
             "Workload: Y = X W^T, X F32 [M x cols], W Q8_0 gate/up 12288x4096 and down 4096x12288, M = 16, 40, 64; each product over "
             ">= 512 MB of rotated weight copies. The contraction runs as bf16 MFMA on three exact limbs of x (3x the flops of the "
             "product, tokens padded to 16).", "",
             "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + GEMM_PROFILE_CMDS + ["```", "",
             "| Product | Kernel | Trace avg us | Bench kernel us | Bench product us (with the partial sum) | GFLOP/s (product) | "
-            "HBM MB (FETCH_SIZE x2) | Algorithmic MB | MFMA busy % | counted bf16 MFMA flop / issued |", "|---|---|---|---|---|---|---|---|---|---|"]
+            "HBM MB (FETCH_SIZE x2) | Algorithmic MB | MFMA busy % | counted bf16 MFMA flop / issued | VGPRs a lane | "
+            "Waves a SIMD at most (registers / LDS) |", "|---|---|---|---|---|---|---|---|---|---|---|---|"]
     text += rows
     text += ["", f"MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). Counted flop = "
              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512; issued = 2 x 3 limbs x the token tiles the kernel runs (whole groups of MG "
              "tiles of 16: at M = 40, 4 tiles, one of them all padding) x rows x cols. Counters are per (kernel, grid): "
-             "products that launch the same kernel on the same grid share one average.", ""]
+             "products that launch the same kernel on the same grid share one average. VGPRs a lane from the library's gfx950 "
+             "code object; the waves a SIMD they allow (512 registers a lane) and those the workgroup's LDS allows (160 KiB a CU, "
+             "the LDS from the kernel trace), at most 8.", ""]
     if stall:
         dh = None
         for l in open(os.path.join(run_dir, "gprof_sq.log")) if os.path.exists(os.path.join(run_dir, "gprof_sq.log")) else []:
@@ -865,10 +929,12 @@ def summarize_verify(run_dir, out=VERIFY_PROFILE, xcds=8, simds=1024):
     from collections import defaultdict
 
     line = json.loads(next(l for l in open(os.path.join(run_dir, "vprof_stats.log")) if l.startswith('{"verify"')))["verify"]
-    trace = defaultdict(list)
+    trace, wg_shape = defaultdict(list), {}
     for r in csv.DictReader(open(os.path.join(run_dir, "vprof_stats", "run_kernel_trace.csv"))):
         g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
         trace[(_kname(r["Kernel_Name"]), g)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        wg_shape[(_kname(r["Kernel_Name"]), g)] = (int(r.get("LDS_Block_Size") or 0), int(r.get("Workgroup_Size_X") or 64))
+    regs = kernel_registers()
     cnt = defaultdict(lambda: defaultdict(list))
     for sub in ("vprof_fetch", "vprof_sq"):
         for r in csv.DictReader(open(os.path.join(run_dir, sub, "run_counter_collection.csv"))):
@@ -891,22 +957,25 @@ def summarize_verify(run_dir, out=VERIFY_PROFILE, xcds=8, simds=1024):
                         f"{100 * alg_bytes(r_, c_, t, pair) / k['kernel_us'] / 1e3 / HBM_PEAK_GBS:.1f} | {2.0 * mean(c.get('FETCH_SIZE', [])) * 1024 / 1e6:.1f} | "
                         f"{alg_bytes(r_, c_, t, pair) / 1e6:.1f} | {64 * valu / weights:.2f} | {100 * 4 * valu / simd_cycles:.1f} | "
                         f"{64 * mfma / weights:.3f} | {100 * mean(c.get('SQ_VALU_MFMA_BUSY_CYCLES', [])) / simd_cycles:.1f} | "
-                        f"{4 * mean(c.get('SQ_WAVE_CYCLES', [])) / simd_cycles:.2f} | {100 * mean(c.get('SQ_WAIT_INST_ANY', [])) / mean(c.get('SQ_WAVE_CYCLES', [])):.1f} |")
+                        f"{4 * mean(c.get('SQ_WAVE_CYCLES', [])) / simd_cycles:.2f} | {100 * mean(c.get('SQ_WAIT_INST_ANY', [])) / mean(c.get('SQ_WAVE_CYCLES', [])):.1f} | "
+                        f"{occupancy_cells(regs, k['kernel'], *wg_shape.get(key, (0, 64)))} |")
     text = ["# Speculative-verify products at 9B shapes, M = 2..4 tokens (rocprofv3)", "",
             "Workload: the fused gate+up pair SiLU(X Wg^T) * (X Wu^T), 2 x 12288x4096, then down 4096x12288, X F32 [M x cols], "
             "scales d = binary16(lognormal(ln 0.002, 1)), each product over >= 512 MB of rotated weight copies.", "",
             "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + VERIFY_PROFILE_CMDS + ["```", "",
             "| M | Product | Kernel | Trace avg us | Bench kernel us | % of HBM peak | HBM MB (FETCH_SIZE x2) | Algorithmic MB | "
             "VALU instructions a weight (x64 lanes) | VALU issue % of SIMD cycles | MFMA instructions a weight (x64) | MFMA busy % of SIMD cycles | "
-            "Waves a SIMD | Wave cycles waiting % |",
-            "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+            "Waves a SIMD | Wave cycles waiting % | VGPRs a lane | Waves a SIMD at most (registers / LDS) |",
+            "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
     text += rows
     text += ["", f"VALU instructions a weight = SQ_INSTS_VALU x 64 lanes / weights (the pair counts both matrices; MFMA instructions are "
              "counted in it too). MFMA instructions a weight = SQ_INSTS_MFMA x 64 / weights (v_mfma_f32_4x4x1_16b_f32 takes 64 weights, 1.0); "
              "MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES over the SIMD cycles below. VALU issue % = "
              f"SQ_INSTS_VALU x 4 cycles (a wave64 instruction on a 16-lane SIMD) / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). "
              "Waves a SIMD = SQ_WAVE_CYCLES (counted in quad-cycles, so x 4) over the same SIMD cycles; wave cycles waiting = "
-             "SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (both in quad-cycles). Counters are per (kernel, grid).", ""]
+             "SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (both in quad-cycles). Counters are per (kernel, grid). VGPRs a lane from the "
+             "library's gfx950 code object (its metadata); the waves a SIMD they allow (512 registers a lane), and those the "
+             "workgroup's LDS allows (160 KiB a CU, from the kernel trace), at most 8.", ""]
     open(out, "w").write("\n".join(text))
     print(f"wrote {out}")
 

@@ -23,15 +23,17 @@ def _csv(path, fields, rows):
         w.writerows(rows)
 
 
-def _trace(path, launches):
-    """launches: (kernel name, grid threads, [durations in us])"""
+def _trace(path, launches, wg=None):
+    """launches: (kernel name, grid threads, [durations in us]); wg: {kernel name: (LDS bytes, workgroup threads)}"""
     rows, t = [], 1000
     for name, grid, durs in launches:
+        lds, threads = (wg or {}).get(name, (0, 256))
         for d in durs:
             rows.append({"Kernel_Name": f"void {name}(unsigned char const*, long)", "Grid_Size_X": grid, "Grid_Size_Y": 1, "Grid_Size_Z": 1,
-                         "Start_Timestamp": t, "End_Timestamp": t + int(round(d * 1000))})
+                         "Start_Timestamp": t, "End_Timestamp": t + int(round(d * 1000)), "LDS_Block_Size": lds, "Workgroup_Size_X": threads})
             t += 100000
-    _csv(path, ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp", "End_Timestamp"], rows)
+    _csv(path, ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp", "End_Timestamp", "LDS_Block_Size", "Workgroup_Size_X"],
+         rows)
 
 
 def _counters(path, values):
@@ -69,15 +71,21 @@ def test_decode_summary_matches_kernel_and_grid(tmp_path):
     assert "Dominant kernel" in text and "7.2 us per launch" in text
 
 
-def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path):
+def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path, monkeypatch):
+    """Per (kernel, grid): trace mean, bench times, counted/issued MFMA work, and the occupancy cells:
+    the code object's VGPRs (here stubbed) give 512 // 128 = 4 waves a SIMD, the x-resident
+    workgroup's 113 KiB of LDS one workgroup a CU, 16 waves: 4 a SIMD; the streaming one's 76 KiB
+    two, 8 a SIMD (at most 8)."""
     run = tmp_path / "run"
     xr, mf = "gemm_xres<2, 16, 8>", "gemm_mfma<3, 1, 2, 16>"
+    monkeypatch.setattr(bench, "kernel_registers", lambda *a, **k: {xr: (128, 0, 54, 0), mf: (96, 0, 60, 0)})
     shapes = {"M16 12288x4096": (xr, 245760, 18.0, 12288, 4096, 16), "M16 4096x12288": (xr, 262144, 19.0, 4096, 12288, 16),
               "M40 12288x4096": (mf, 245760, 27.0, 12288, 4096, 40)}
     line = {"prompt_gemm": {s: {"kernel": n, "grid": g, "kernel_us": us, "product_us": us + 1, "GFLOPS": 1.0} for s, (n, g, us, _, _, _) in shapes.items()}}
     os.makedirs(run)
     (run / "gprof_stats.log").write_text(json.dumps(line) + "\n")
-    _trace(str(run / "gprof_stats" / "run_kernel_trace.csv"), [(xr, 245760, [17.0, 17.4]), (xr, 262144, [18.5]), (mf, 245760, [26.0, 28.0])])
+    _trace(str(run / "gprof_stats" / "run_kernel_trace.csv"), [(xr, 245760, [17.0, 17.4]), (xr, 262144, [18.5]), (mf, 245760, [26.0, 28.0])],
+           wg={xr: (115712, 1024), mf: (77824, 1024)})
     # issued bf16 MFMA flop = 2 x 3 limbs x the token tiles run x rows x cols; the counter counts 512 flop a MOP
     mops = {(n, g): 2.0 * 3 * (16 * (1 if n == xr else 3)) * r * c / 512 for n, g, _, r, c, _ in shapes.values()}
     _counters(str(run / "gprof_fetch" / "run_counter_collection.csv"), [(n, g, "FETCH_SIZE", [30000.0]) for (n, g) in mops])
@@ -90,8 +98,9 @@ def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path):
     rows = {l.split("|")[1].strip(): [c.strip() for c in l.split("|")[2:-1]] for l in out.read_text().splitlines() if l.startswith("| M")}
     assert rows["M16 12288x4096"][1] == "17.20" and rows["M16 4096x12288"][1] == "18.50" and rows["M40 12288x4096"][1] == "27.00"
     for s in shapes:
-        assert rows[s][-1] == "1.000", s  # counted / issued: one token tile for gemm_xres, three for gemm_mfma<3, ...>
-        assert rows[s][-2] == "10.0", s   # MFMA busy: 1024 cycles over (80 / 8 XCDs x 1024 SIMDs)
+        assert rows[s][-3] == "1.000", s  # counted / issued: one token tile for gemm_xres, three for gemm_mfma<3, ...>
+        assert rows[s][-4] == "10.0", s   # MFMA busy: 1024 cycles over (80 / 8 XCDs x 1024 SIMDs)
+    assert rows["M16 12288x4096"][-2:] == ["128", "4 / 4"] and rows["M40 12288x4096"][-2:] == ["96", "5 / 8"]
 
 
 def test_gemm_stall_table_by_hand(tmp_path):
