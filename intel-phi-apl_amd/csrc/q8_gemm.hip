@@ -506,12 +506,6 @@ struct gemm_plan {
     int ks, cps;
 };
 
-/* The K split of a rows x cols matrix: ks splits of cps ranges of XRES_KP block pairs (the last may
- * hold fewer), a function of the shape alone, so that a token's output has the same bits whatever
- * the number of tokens it is computed with (5 to 64 a launch, and every 64-token launch of a longer
- * X). As many splits as fill the device with one resident round of the x-resident kernel's
- * workgroups (256 rows each), fewer if the partials of a 64-token launch would not fit the
- * workspace. ks_force > 0 sets the split count instead (a test hook: other splits, other bits). */
 /* resident workgroups of the x-resident kernel with nw waves (16 or 12) */
 static long resident_xres(int nw)
 {
@@ -519,6 +513,13 @@ static long resident_xres(int nw)
     return nw == 12 ? resident(gemm_xres<XRES_KP, 12, XRES_SC>, 64 * 12, n12) : resident(gemm_xres<XRES_KP, 16, XRES_SC>, 64 * 16, n16);
 }
 
+/* The K split of a rows x cols matrix: ks splits of cps ranges of XRES_KP block pairs (the last may
+ * hold fewer), a function of the shape alone (nw comes from the shape too), so that a token's
+ * output has the same bits whatever the number of tokens it is computed with (5 to 64 a launch,
+ * and every 64-token launch of a longer X). As many splits as fill the device with one resident
+ * round of the x-resident kernel's workgroups (16 nw rows each), fewer if the partials of a
+ * 64-token launch would not fit the workspace. ks_force > 0 sets the split count instead (a test
+ * hook: other splits, other bits). */
 static void split_of(long rows, long cols, int nw, int ks_force, int *ks, int *cps)
 {
     const long tiles = (rows + 16L * nw - 1) / (16L * nw);
