@@ -498,10 +498,14 @@ def gguf_load(b):
 
 
 def layers_2b(b):
-    """Config 2: 24 layers of QKV 3072x2048, out 2048x2048, gate/up 6144x2048 (fused), down 2048x6144."""
+    """Config 2: 24 layers of QKV 3072x2048, out 2048x2048, gate/up 6144x2048 (fused), down 2048x6144,
+    one graph; beside it its floor, a graph of the same 96 positions as pure reads of each product's
+    bytes on its own grid (rt_q8_read_dev), as for the 9B token."""
     H, F, Q = 2048, 6144, 2048 + 2 * 512
     layers = [(b.matrix(Q, H), b.matrix(H, H), b.matrix(F, H), b.matrix(F, H), b.matrix(H, F)) for _ in range(24)]
     xh, h, yq, yo, yd = b.vec(H), b.vec(F), b.vec(Q), b.vec(H), b.vec(H)
+    sink = b.vec(F)  # a word a workgroup: fewer workgroups than the largest product's rows
+    V = c.c_void_p
 
     def run():
         for qkv, o, g, u, d in layers:
@@ -510,17 +514,29 @@ def layers_2b(b):
             b.pair(g, u, F, H, xh, 1, h)
             b.gemm(d, H, F, h, 1, yd)
 
+    def floor():
+        for qkv, o, g, u, d in layers:
+            b.lib.rt_q8_read_dev(b.R, V(qkv), None, Q, H, V(xh), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(o), None, H, H, V(xh), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(g), V(u), F, H, V(xh), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(d), None, H, F, V(h), V(sink))
+
     per = 24 * (alg_bytes(Q, H, 1) + alg_bytes(H, H, 1) + alg_bytes(F, H, 1, pair=True) + alg_bytes(H, F, 1))
-    b.lib.rt_graph_begin(b.R)
-    run()
-    g = b.lib.rt_graph_end(b.R)
-    b.lib.rt_graph_launch(b.R, c.c_void_p(g))
-    ms = b.timed(lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(g)), 20)
-    b.lib.rt_graph_free(b.R, c.c_void_p(g))
+    out = {}
+    for key, fn in (("", run), ("floor_", floor)):
+        b.lib.rt_graph_begin(b.R)
+        fn()
+        g = b.lib.rt_graph_end(b.R)
+        b.lib.rt_graph_launch(b.R, V(g))
+        ms = b.timed(lambda: b.lib.rt_graph_launch(b.R, V(g)), 20)
+        b.lib.rt_graph_free(b.R, V(g))
+        out[f"{key}us_per_pass"] = round(1e3 * ms, 2)
+        out[f"{key}GB/s"] = round(per / ms / 1e6, 1)
     for L in layers:
         for w in L:
             b.rt.free(w)
-    return {"us_per_pass": round(1e3 * ms, 2), "GB/s": round(per / ms / 1e6, 1), "bytes": per}
+    out["bytes"] = per
+    return out
 
 
 def cpu_baseline(b, layer, seconds):
