@@ -264,18 +264,30 @@ def decode_9b(b, steps, warmup):
     return per_token, ms_graph, ms_eager, kernels, roof, layers
 
 
+def read_floor_us(b, ws, rows, cols, x):
+    """Mean duration of the pure read of each rotated copy on its product's grid (rt_q8_read_dev):
+    the floor the product's kernel is held against."""
+    sink = b.vec(rows)
+    V = c.c_void_p
+    reads = lambda: [b.lib.rt_q8_read_dev(b.R, V(w), None, rows, cols, V(x), V(sink)) for w in ws]  # noqa: E731
+    reads()
+    return statistics.fmean(next(iter(b.ktimes(reads, 4).values())))
+
+
 def single_gemv(b):
-    """Config 1's shape on the GPU: 4096x4096, rotated through >= 512 MB of copies."""
+    """Config 1's shape on the GPU: 4096x4096, rotated through >= 512 MB of copies, and its floor."""
     ws = rotation(b, 4096, 4096)
     x, y = b.vec(4096), b.vec(4096)
     [b.gemm(w, 4096, 4096, x, 1, y) for w in ws]  # one untimed pass: the copies' first touch and the kernel's first launch
     kt = b.ktimes(lambda: [b.gemm(w, 4096, 4096, x, 1, y) for w in ws], 4)
     us = statistics.fmean(next(iter(kt.values())))
     ms = b.timed(lambda: [b.gemm(w, 4096, 4096, x, 1, y) for w in ws], 4) / len(ws)
+    floor = read_floor_us(b, ws, 4096, 4096, x)
     for w in ws:
         b.rt.free(w)
     gb = alg_bytes(4096, 4096, 1)
-    return {"kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "back_to_back_us": round(1e3 * ms, 3), "copies": len(ws)}
+    return {"kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "back_to_back_us": round(1e3 * ms, 3), "floor_us": round(floor, 3),
+            "copies": len(ws)}
 
 
 def draft_head(b):
@@ -285,10 +297,12 @@ def draft_head(b):
     kt = b.ktimes(lambda: [b.gemm(w, DRAFT, HIDDEN, x, 1, y) for w in ws], 4)
     us = statistics.fmean(next(iter(kt.values())))
     kname, grid = b.knames[next(iter(kt))]
+    floor = read_floor_us(b, ws, DRAFT, HIDDEN, x)
     for w in ws:
         b.rt.free(w)
     gb = alg_bytes(DRAFT, HIDDEN, 1)
-    return {"rows": DRAFT, "kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "copies": len(ws), "kernel": kname, "grid": grid}
+    return {"rows": DRAFT, "kernel_us": round(us, 3), "GB/s": round(gb / us / 1e3, 1), "floor_us": round(floor, 3), "copies": len(ws), "kernel": kname,
+            "grid": grid}
 
 
 def prompt_gemm(b):
