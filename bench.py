@@ -156,11 +156,11 @@ def token_9b(b):
     def floor():
         """the same 129 positions, each the product's loads on its grid and nothing else (rt_q8_read_dev)"""
         for L in layers:
-            b.lib.rt_q8_read_dev(b.R, V(L["qkv"]), None, QKV, HIDDEN, V(xh), V(sink))
-            b.lib.rt_q8_read_dev(b.R, V(L["out"]), None, HIDDEN, HIDDEN, V(xa), V(sink))
-            b.lib.rt_q8_read_dev(b.R, V(L["gate"]), V(L["up"]), FFN, HIDDEN, V(xh), V(sink))
-            b.lib.rt_q8_read_dev(b.R, V(L["down"]), None, HIDDEN, FFN, V(h), V(sink))
-        b.lib.rt_q8_read_dev(b.R, V(head), None, VOCAB, HIDDEN, V(xh), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["qkv"]), None, QKV, HIDDEN, V(xh), HIDDEN, 1, V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["out"]), None, HIDDEN, HIDDEN, V(xa), HIDDEN, 1, V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["gate"]), V(L["up"]), FFN, HIDDEN, V(xh), HIDDEN, 1, V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(L["down"]), None, HIDDEN, FFN, V(h), FFN, 1, V(sink))
+        b.lib.rt_q8_read_dev(b.R, V(head), None, VOCAB, HIDDEN, V(xh), HIDDEN, 1, V(sink))
 
     token.floor = floor
     per_token = LAYERS * (alg_bytes(QKV, HIDDEN, 1) + alg_bytes(HIDDEN, HIDDEN, 1) + alg_bytes(FFN, HIDDEN, 1, pair=True) +
@@ -269,7 +269,7 @@ def read_floor_us(b, ws, rows, cols, x):
     the floor the product's kernel is held against."""
     sink = b.vec(rows)
     V = c.c_void_p
-    reads = lambda: [b.lib.rt_q8_read_dev(b.R, V(w), None, rows, cols, V(x), V(sink)) for w in ws]  # noqa: E731
+    reads = lambda: [b.lib.rt_q8_read_dev(b.R, V(w), None, rows, cols, V(x), cols, 1, V(sink)) for w in ws]  # noqa: E731
     reads()
     return statistics.fmean(next(iter(b.ktimes(reads, 4).values())))
 
@@ -341,18 +341,29 @@ def prompt_gemm(b):
 def verify_path(b):
     """Config 5: M = 2..4 tokens, fused gate+up (2 x 12288x4096) then down 4096x12288, d lognormal(ln 0.002, 1),
     over rotated weight sets; each kernel's mean duration (events on its launches) over three passes
-    after one untimed pass (the first launches run on cold page tables and code: up to 2x slower)."""
+    after one untimed pass (the first launches run on cold page tables and code: up to 2x slower),
+    and beside it its floor: the same loads at M tokens on the product's own grid, no arithmetic
+    (rt_q8_read_dev), timed the same way."""
     kw = dict(dist=1, mu=float(np.log(0.002)), sigma=1.0)
     per = 2 * q8_bytes(FFN, HIDDEN) + q8_bytes(HIDDEN, FFN)
     n = max(2, -(-MALL_ROTATE_BYTES // per))
     sets = [(b.matrix(FFN, HIDDEN, **kw), b.matrix(FFN, HIDDEN, **kw), b.matrix(HIDDEN, FFN, **kw)) for _ in range(n)]
     x, h, y = b.vec(4 * HIDDEN), b.vec(4 * FFN), b.vec(4 * HIDDEN)
+    sink = b.vec(FFN)
+    V = c.c_void_p
     out = {}
     for m in (2, 3, 4):
         def step():
             for g, u, d in sets:
                 b.pair(g, u, FFN, HIDDEN, x, m, h)
                 b.gemm(d, HIDDEN, FFN, h, m, y)
+
+        def reads():
+            for g, u, d in sets:
+                b.lib.rt_q8_read_dev(b.R, V(g), V(u), FFN, HIDDEN, V(x), HIDDEN, m, V(sink))
+                b.lib.rt_q8_read_dev(b.R, V(d), None, HIDDEN, FFN, V(h), FFN, m, V(sink))
+        reads()
+        floor = {k: statistics.fmean(v) for k, v in b.ktimes(reads, 3).items()}
         step()  # one untimed pass: the copies' first touch and the kernels' first launch
         kt = b.ktimes(step, 3)
         res = {}
@@ -360,9 +371,10 @@ def verify_path(b):
             pair = kind.endswith("pair")
             us = statistics.fmean(v)
             kname, grid = b.knames[(kind, rows, cols, t)]
+            fl = floor.get((kind, rows, cols, t))
             res["fused_gate_up" if pair else "down"] = {"kernel_us": round(us, 3), "GB/s": round(alg_bytes(rows, cols, t, pair) / us / 1e3, 1),
                                                           "pct_hbm": round(100 * alg_bytes(rows, cols, t, pair) / us / 1e3 / HBM_PEAK_GBS, 1),
-                                                          "kernel": kname, "grid": grid}
+                                                          "floor_us": round(fl, 3) if fl else None, "kernel": kname, "grid": grid}
         out[f"M{m}"] = res
     for s in sets:
         for w in s:
@@ -530,10 +542,10 @@ def layers_2b(b):
 
     def floor():
         for qkv, o, g, u, d in layers:
-            b.lib.rt_q8_read_dev(b.R, V(qkv), None, Q, H, V(xh), V(sink))
-            b.lib.rt_q8_read_dev(b.R, V(o), None, H, H, V(xh), V(sink))
-            b.lib.rt_q8_read_dev(b.R, V(g), V(u), F, H, V(xh), V(sink))
-            b.lib.rt_q8_read_dev(b.R, V(d), None, H, F, V(h), V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(qkv), None, Q, H, V(xh), H, 1, V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(o), None, H, H, V(xh), H, 1, V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(g), V(u), F, H, V(xh), H, 1, V(sink))
+            b.lib.rt_q8_read_dev(b.R, V(d), None, H, F, V(h), F, 1, V(sink))
 
     per = 24 * (alg_bytes(Q, H, 1) + alg_bytes(H, H, 1) + alg_bytes(F, H, 1, pair=True) + alg_bytes(H, F, 1))
     out = {}

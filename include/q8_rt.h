@@ -217,14 +217,15 @@ void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed);
  * (16-byte aligned, bytes % 16 == 0): the yardstick the benchmark scales the HBM byte counters by. */
 void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes);
 
-/* The floor of a one-token decode product (a measurement tool, like rt_dev_copy): the loads the
- * product kernel makes for y = W x at one token (x, every row's weights and scales, both matrices
- * of the fused pair when w1 != NULL), on the product's own grid, and no arithmetic but a checksum:
- * workgroup b stores the wrapping sum of every 32-bit word it read (scales zero-extended; each
- * workgroup reads all of x, each scale is read by two lanes) to sink[b]. sink: device, `rows`
- * unsigned (a workgroup takes at least one row; the entries past the grid are not written). For
- * cols a multiple of 1024 at the grids the decode kernel uses; any other shape aborts. */
-void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, long cols, const float *x, unsigned *sink);
+/* The floor of a decode product (a measurement tool, like rt_dev_copy): the loads the product
+ * kernel makes for Y = X W^T at t tokens, 1 to 4 (x rows x_stride floats apart; every row's
+ * weights and scales, both matrices of the fused pair when w1 != NULL), on the product's own grid,
+ * and no arithmetic but a checksum: workgroup b stores the wrapping sum of every 32-bit word it
+ * read (scales zero-extended; each workgroup reads all of x, each scale is read by two lanes) to
+ * sink[b]. sink: device, `rows` unsigned (a workgroup takes at least one row; the entries past the
+ * grid are not written). For the decode token's shapes at one token and the 9B verify shapes
+ * (the fused pair 12288 x 4096, down 4096 x 12288) at 2 to 4; any other shape aborts. */
+void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink);
 
 /* The product kernels' primitive conversions on the GPU, lane by lane: o8[i] = fma(x8[i],
  * (float)q[i], c8[i]) with the int8 convert of the weights (n8 % 4 == 0), of[i] = fma(xf[i],

@@ -58,7 +58,7 @@ _SIGS = {
     "rt_q8_repack_dev": (None, [_vp, _vp, _long, _long, _vp]),
     "rt_f32_fill_dev": (None, [_vp, _vp, _long, _u64]),
     "rt_dev_copy": (None, [_vp, _vp, _vp, _long]),
-    "rt_q8_read_dev": (None, [_vp, _vp, _vp, _long, _long, _vp, _vp]),
+    "rt_q8_read_dev": (None, [_vp, _vp, _vp, _long, _long, _vp, _long, _long, _vp]),
     "rt_q8_row": (None, [_vp, _long, _long, _vp]),
     "rt_q8_rows_dev": (None, [_vp, _vp, _long, _vp, _long, _vp]),
     "rt_argmax_dev": (None, [_vp, _vp, _long, _vp]),

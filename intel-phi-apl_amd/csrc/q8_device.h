@@ -269,11 +269,11 @@ void q8_launch_repack(q8_stream_t stream, const void *q8, long rows, long cols, 
 /* Synthetic GGUF rows and F32 values on the device. */
 void q8_launch_fill(q8_stream_t stream, void *dst, long rows, long cols, uint64_t seed, int dist, float mu, float sigma);
 void q8_launch_fill_f32(q8_stream_t stream, float *dst, long n, uint64_t seed);
-/* The decode product's loads at one token, nothing computed: the floor of a product of that shape
- * (w1: the fused pair's two matrices). sink[b] (device, rows entries) receives workgroup b's
- * checksum of the words it read (added, wrapping). 0, or -1 when the shape has no such kernel
- * (nothing launched). */
-int q8_launch_read(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, unsigned *sink);
+/* The decode product's loads at t tokens (x rows x_stride apart), nothing computed: the floor of a
+ * product of that shape (w1: the fused pair's two matrices). sink[b] (device, rows entries)
+ * receives workgroup b's checksum of the words it read (added, wrapping). 0, or -1 when the shape
+ * has no such kernel (nothing launched). */
+int q8_launch_read(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink);
 /* dst = src, n16 16-byte words, both device. */
 void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16);
 /* *flag = seq once the kernels before it on the stream are done; flag in pinned host memory. */

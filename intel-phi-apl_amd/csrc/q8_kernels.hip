@@ -949,17 +949,19 @@ void q8_launch_copy(q8_stream_t stream, void *dst, const void *src, long n16)
  * added, the NW waves' through LDS, and one thread stores the workgroup's sum to sink[blockIdx.x]:
  * the product's own end (a sum over lanes and waves, one barrier, a store) without its arithmetic.
  * The sums make the loads live and give a checksum the tests recompute. */
-template <int RW, int NW, int PAIR>
+template <int RW, int NW, int PAIR, int MT>
 __global__ __launch_bounds__(64 * NW) void read_k(const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, long cols, const float *__restrict__ x,
-                                                  unsigned *sink)
+                                                  long x_stride, unsigned *sink)
 {
     constexpr int P = PAIR + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const long u0 = (long)wave * 64 + lane, r0 = (long)blockIdx.x * RW;
-    uint4 xv[4];
+    uint4 xv[MT][4];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        xv[c] = *(const uint4 *)(x + 16 * u0 + 4 * c);
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            xv[m][c] = *(const uint4 *)(x + m * x_stride + 16 * u0 + 4 * c);
     uint4 q[RW][P];
     uint16_t dh[RW][P];
 #pragma unroll
@@ -973,8 +975,10 @@ __global__ __launch_bounds__(64 * NW) void read_k(const uint8_t *__restrict__ w0
     __builtin_amdgcn_sched_barrier(0);
     unsigned acc = 0;
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-        acc += xv[c].x + xv[c].y + xv[c].z + xv[c].w;
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            acc += xv[m][c].x + xv[m][c].y + xv[m][c].z + xv[m][c].w;
 #pragma unroll
     for (int r = 0; r < RW; r++)
 #pragma unroll
@@ -996,24 +1000,29 @@ __global__ __launch_bounds__(64 * NW) void read_k(const uint8_t *__restrict__ w0
     }
 }
 
-/* the decode kernel's grid for a product at one token (gemv_choose), or false when the decode
- * kernel would loop over K (cols not a multiple of 1024 in its instances) */
-int q8_launch_read(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, unsigned *sink)
+/* the decode kernel's grid for a product at t tokens (gemv_choose), or false when no instance
+ * takes it: at one token the shapes of the decode tokens' products (cols a multiple of 1024), at 2
+ * to 4 the 9B verify shapes (the fused pair 12288 x 4096 and down 4096 x 12288) */
+int q8_launch_read(q8_stream_t stream, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink)
 {
     const long kb = cols % 1024 ? 0 : cols / 1024;
+    if (t < 1 || t > 4)
+        return -1;
     int rw, nw;
-    gemv_choose(w1 != nullptr, 1, rows, kb, &rw, &nw);
+    gemv_choose(w1 != nullptr, (int)t, rows, kb, &rw, &nw);
     if (!kb || rows % rw || kb != nw)
         return -1;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *a = (const uint8_t *)w0, *b = (const uint8_t *)w1;
-#define RD(RW_, NW_, P_)                                                                                               \
-    if (rw == RW_ && nw == NW_ && (b != nullptr) == (P_ == 1)) {                                                       \
-        Q8_LAUNCH(q8_time_name("read_k", 3, RW_, NW_, P_), (read_k<RW_, NW_, P_>), dim3((unsigned)(rows / RW_)), dim3(64 * NW_), s, a, b, cols, x,  \
-                  sink);                                                                                               \
+#define RD(RW_, NW_, P_, MT_)                                                                                          \
+    if (t == MT_ && rw == RW_ && nw == NW_ && (b != nullptr) == (P_ == 1)) {                                           \
+        Q8_LAUNCH(q8_time_name("read_k", 4, RW_, NW_, P_, MT_), (read_k<RW_, NW_, P_, MT_>), dim3((unsigned)(rows / RW_)), dim3(64 * NW_), s, a, b,   \
+                  cols, x, x_stride, sink);                                                                            \
         return 0;                                                                                                      \
     }
-    RD(8, 4, 0) RD(8, 12, 0) RD(4, 4, 1) RD(8, 2, 0) RD(4, 2, 0) RD(2, 2, 0) RD(4, 6, 0) RD(2, 6, 0) RD(2, 2, 1) RD(4, 2, 1) RD(8, 6, 0)
+    RD(8, 4, 0, 1) RD(8, 12, 0, 1) RD(4, 4, 1, 1) RD(8, 2, 0, 1) RD(4, 2, 0, 1) RD(2, 2, 0, 1) RD(4, 6, 0, 1) RD(2, 6, 0, 1) RD(2, 2, 1, 1)
+    RD(4, 2, 1, 1) RD(8, 6, 0, 1)
+    RD(8, 4, 1, 2) RD(8, 4, 1, 3) RD(8, 4, 1, 4) RD(16, 12, 0, 2) RD(16, 12, 0, 3) RD(16, 12, 0, 4)
 #undef RD
     return -1;
 }

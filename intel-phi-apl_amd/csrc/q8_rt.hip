@@ -1167,7 +1167,7 @@ void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes)
     launched("the copy");
 }
 
-void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, long cols, const float *x, unsigned *sink)
+void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink)
 {
     ctx *c = get(R, "rt_q8_read_dev");
     check_shape(c, "rt_q8_read_dev", w0, rows, cols);
@@ -1175,12 +1175,14 @@ void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, lon
         check_shape(c, "rt_q8_read_dev", w1, rows, cols);
     check_dev_ptr("rt_q8_read_dev", x, "x");
     check_dev_ptr("rt_q8_read_dev", sink, "sink");
-    const bool timed = kt_begin(c, w1 ? RT_K_GEMV_PAIR : RT_K_GEMV, rows, cols, 1);
-    if (q8_launch_read((q8_stream_t)c->stream, w0, w1, rows, cols, x, sink) != 0) {
+    if (t < 1 || t > 4 || (t > 1 && (x_stride < cols || x_stride % 4)))
+        fail("rt_q8_read_dev", "needs 1 to 4 tokens, x rows at least cols floats apart (a multiple of 4)");
+    const bool timed = kt_begin(c, w1 ? RT_K_GEMV_PAIR : RT_K_GEMV, rows, cols, t);
+    if (q8_launch_read((q8_stream_t)c->stream, w0, w1, rows, cols, x, x_stride, t, sink) != 0) {
         if (timed)
             kt_cancel(c);
-        failf("rt_q8_read_dev", "no read kernel for %ld x %ld%s (the decode kernel's one-token grids, cols a multiple of 1024)", rows, cols,
-              w1 ? " (pair)" : "");
+        failf("rt_q8_read_dev", "no read kernel for %ld x %ld%s at %ld tokens (the decode kernel's grids for the decode token's shapes at one "
+              "token, and for the 9B verify shapes at 2 to 4)", rows, cols, w1 ? " (pair)" : "", t);
     }
     launched("the read");
 }

@@ -768,13 +768,15 @@ def test_c_drop_in_caller(tmp_path):
     assert p.returncode == 0, p.stdout + p.stderr
 
 
-@pytest.mark.parametrize("rows,cols,pair", [(4096, 4096, False), (6144, 4096, False), (4096, 12288, False), (12288, 4096, True),
-                                            (3072, 2048, False), (6144, 2048, True), (2048, 6144, False), (151936, 4096, False)])
-def test_read_floor_checksum(rt, rows, cols, pair):
-    """rt_q8_read_dev (the decode product's loads on its grid, no arithmetic: the floor the benchmark
-    sets each product against) reads every byte of the matrix or matrices: its wrapping sum of the
-    32-bit words read equals numpy's, with x = 0 (each scale is read by two lanes)."""
-    rng = np.random.default_rng(rows + cols + pair)
+@pytest.mark.parametrize("rows,cols,pair,t", [(4096, 4096, False, 1), (6144, 4096, False, 1), (4096, 12288, False, 1), (12288, 4096, True, 1),
+                                              (3072, 2048, False, 1), (6144, 2048, True, 1), (2048, 6144, False, 1), (151936, 4096, False, 1),
+                                              (12288, 4096, True, 2), (12288, 4096, True, 4), (4096, 12288, False, 3)])
+def test_read_floor_checksum(rt, rows, cols, pair, t):
+    """rt_q8_read_dev (the decode product's loads on its grid at t tokens, no arithmetic: the floor
+    the benchmark sets each product against) reads every byte of the matrix or matrices: its
+    wrapping sum of the 32-bit words read equals numpy's, with x = 0 (each scale is read by two
+    lanes)."""
+    rng = np.random.default_rng(rows + cols + pair + 10 * t)
     mats = [synth.q8_rows(rng, rows, cols) for _ in range(2 if pair else 1)]
     want = 0
     for q8 in mats:
@@ -783,8 +785,9 @@ def test_read_floor_checksum(rt, rows, cols, pair):
     ws = [rt.upload(q8, rows, cols) for q8 in mats]
     try:
         with Dev(rt) as d:
-            dx, sink = d.put(np.zeros(cols, np.float32)), d.put(np.zeros(rows, np.uint32))
-            rt.lib.rt_q8_read_dev(rt.R, c.c_void_p(ws[0]), c.c_void_p(ws[1]) if pair else None, rows, cols, c.c_void_p(dx), c.c_void_p(sink))
+            dx, sink = d.put(np.zeros(t * cols, np.float32)), d.put(np.zeros(rows, np.uint32))
+            rt.lib.rt_q8_read_dev(rt.R, c.c_void_p(ws[0]), c.c_void_p(ws[1]) if pair else None, rows, cols, c.c_void_p(dx), cols, t,
+                                  c.c_void_p(sink))
             got = d.get(sink, (rows,), np.uint32)
     finally:
         for w in ws:
