@@ -93,8 +93,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
     const int split = (int)(blockIdx.x % ks);
     const long tt0 = (long)blockIdx.y * MT;
     const long rt0 = (tile * NW + wave) * RT;
-    /* a wave past the last row tile reads row tile 0 and contributes nothing */
+    /* a row tile past the last one (of a wave's RT, any but the first may be) reads row tile 0
+     * and contributes nothing */
     const bool live = rt0 < rows / 16;
+    auto live_r = [&](int r) { return rt0 + r < rows / 16; };
     const int n = lane & 15, kq = lane >> 4;
 
     /* issue every load of the range starting at pair c0. All are unconditional, from indices
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 /* the row tile at a uniform base, the lane's row and 16 bytes at a 32-bit offset */
-                const uint8_t *wt = w + q8s_row_q(live ? (rt0 + r) * 16 : 0, cols) + 64L * c;
+                const uint8_t *wt = w + q8s_row_q(live_r(r) ? (rt0 + r) * 16 : 0, cols) + 64L * c;
                 S.q[p][r] = *(const uint4 *)(wt + (unsigned)(n * cols + 16 * kq));
             }
         }
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
 #pragma unroll
         for (int p = 0; p < KP; p++) {
             const int c = c0 + p;
-            const bool ok0 = live && c < np, ok1 = live && 2 * c + 1 < nb; /* block 2c, block 2c+1 */
+            const bool ok0 = c < np, ok1 = 2 * c + 1 < nb; /* block 2c, block 2c+1 */
             bf16x8 wb[2][RT];
             float d[2][RT];
 #pragma unroll
@@ -187,8 +189,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
                 wb[1][r] = q8_bf16(s02[1], s13[1]);
                 const int lr = (wave * RT + r) * 16 + n; /* the lane's row in the workgroup */
                 const float d0 = q8_half(dl[lr * 2 * KP + 2 * p]), d1 = q8_half(dl[lr * 2 * KP + 2 * p + 1]);
-                d[0][r] = ok0 ? d0 : 0.0f;
-                d[1][r] = ok1 ? d1 : 0.0f;
+                d[0][r] = ok0 && live_r(r) ? d0 : 0.0f;
+                d[1][r] = ok1 && live_r(r) ? d1 : 0.0f;
             }
 #pragma unroll
             for (int h = 0; h < 2; h++) {
@@ -249,7 +251,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
         return;
     const long tp = (t + 15) / 16 * 16;
 #pragma unroll
-    for (int r = 0; r < RT; r++)
+    for (int r = 0; r < RT; r++) {
+        if (!live_r(r))
+            continue;
 #pragma unroll
         for (int m = 0; m < MT; m++)
 #pragma unroll
@@ -263,6 +267,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
                     part[((long)split * tp + tok) * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
                 }
             }
+    }
 }
 
 /* One token tile (t <= 16) with x resident in LDS. A workgroup of NW waves owns NW row tiles
