@@ -264,12 +264,12 @@ def decode_9b(b, steps, warmup):
     return per_token, ms_graph, ms_eager, kernels, roof, layers
 
 
-def read_floor_us(b, ws, rows, cols, x):
-    """Mean duration of the pure read of each rotated copy on its product's grid (rt_q8_read_dev):
-    the floor the product's kernel is held against."""
+def read_floor_us(b, ws, rows, cols, x, t=1):
+    """Mean duration of the pure read of each rotated copy on its product's grid at t tokens
+    (rt_q8_read_dev; x holds t rows of cols floats): the floor the product's kernel is held against."""
     sink = b.vec(rows)
     V = c.c_void_p
-    reads = lambda: [b.lib.rt_q8_read_dev(b.R, V(w), None, rows, cols, V(x), cols, 1, V(sink)) for w in ws]  # noqa: E731
+    reads = lambda: [b.lib.rt_q8_read_dev(b.R, V(w), None, rows, cols, V(x), cols, t, V(sink)) for w in ws]  # noqa: E731
     reads()
     return statistics.fmean(next(iter(b.ktimes(reads, 4).values())))
 
@@ -312,8 +312,9 @@ def prompt_gemm(b):
     the partials) back to back over the rotated copies, stream events; GFLOPS and GB/s are over
     it. kernel_us: the matrix-core kernel alone (events on its launch). GFLOPS counts
     2*M*rows*cols; mfma_util_kernel is the bf16 MFMA work actually issued (three limbs, tokens
-    padded to 16) over the matrix-core kernel's time, against the dense bf16 peak. Timed after one
-    untimed pass over the copies."""
+    padded to 16) over the matrix-core kernel's time, against the dense bf16 peak. floor_us (M =
+    16): the x-resident kernel's own loads on its grid with no arithmetic (rt_q8_read_dev at 16
+    tokens). Timed after one untimed pass over the copies."""
     out = {}
     for rows, cols in ((FFN, HIDDEN), (HIDDEN, FFN)):
         ws = rotation(b, rows, cols)
@@ -331,6 +332,8 @@ def prompt_gemm(b):
                                           "GB/s": round(alg_bytes(rows, cols, m) / ms / 1e6, 1),
                                           "pct_hbm": round(100 * alg_bytes(rows, cols, m) / ms / 1e6 / HBM_PEAK_GBS, 1),
                                           "mfma_util_kernel": round(issued / us / 1e6 / BF16_PEAK_TFLOPS, 4), "copies": len(ws)}
+            if m <= 16:  # the x-resident kernel's loads on its grid, no arithmetic
+                out[f"M{m} {rows}x{cols}"]["floor_us"] = round(read_floor_us(b, ws, rows, cols, x, m), 3)
         for w in ws:
             b.rt.free(w)
         b.rt.free(x)

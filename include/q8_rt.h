@@ -217,14 +217,19 @@ void rt_f32_fill_dev(struct rt *R, float *dst, long n, uint64_t seed);
  * (16-byte aligned, bytes % 16 == 0): the yardstick the benchmark scales the HBM byte counters by. */
 void rt_dev_copy(struct rt *R, void *dst, const void *src, long bytes);
 
-/* The floor of a decode product (a measurement tool, like rt_dev_copy): the loads the product
- * kernel makes for Y = X W^T at t tokens, 1 to 4 (x rows x_stride floats apart; every row's
- * weights and scales, both matrices of the fused pair when w1 != NULL), on the product's own grid,
- * and no arithmetic but a checksum: workgroup b stores the wrapping sum of every 32-bit word it
- * read (scales zero-extended; each workgroup reads all of x, each scale is read by two lanes) to
- * sink[b]. sink: device, `rows` unsigned (a workgroup takes at least one row; the entries past the
- * grid are not written). For the decode token's shapes at one token and the 9B verify shapes
- * (the fused pair 12288 x 4096, down 4096 x 12288) at 2 to 4; any other shape aborts. */
+/* The floor of a product (a measurement tool, like rt_dev_copy): the loads the product kernel
+ * makes for Y = X W^T at t tokens (x rows x_stride floats apart), on the product's own grid, and
+ * no arithmetic but a checksum.
+ * t = 1 to 4, the decode kernel: every row's weights and scales, both matrices of the fused pair
+ * when w1 != NULL; workgroup b stores the wrapping sum of every 32-bit word it read (scales
+ * zero-extended; each workgroup reads all of x, each scale is read by two lanes) to sink[b]. For
+ * the decode token's shapes at one token and the 9B verify shapes (the fused pair 12288 x 4096,
+ * down 4096 x 12288) at 2 to 4; any other shape aborts.
+ * t = 5 to 16, the x-resident matrix-core kernel (one matrix, w1 NULL): its grid, K split and
+ * loads, every weight word and scale added once and every x word as loaded (each workgroup reads
+ * its K range of x), each workgroup adding its sum to sink[0] (zero it first). Any shape the
+ * product takes.
+ * sink: device, `rows` unsigned (the entries past the grid are not written). */
 void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink);
 
 /* The product kernels' primitive conversions on the GPU, lane by lane: o8[i] = fma(x8[i],

@@ -255,6 +255,11 @@ struct q8_gemm_opts {
 void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
                          const float *res, q8_gemm_opts o);
 long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o);
+/* The floor of the x-resident product at 5 <= t <= 16 tokens: its loads on its grid (the plan for
+ * these options), no arithmetic, a checksum added to sink[0]; -1 when the plan is not the
+ * x-resident kernel. */
+int q8_launch_read_gemm(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink,
+                        q8_gemm_opts o);
 /* y[i] = SiLU(g[i]) * u[i] (the exact fused pair's epilogue). */
 void q8_launch_swiglu_ew(q8_stream_t stream, const float *g, const float *u, long n, float *y);
 /* z[i] = row rows[i] of w dequantised (q * d, exact), i < n; rows and z device arrays; an index

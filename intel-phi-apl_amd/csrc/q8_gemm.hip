@@ -434,6 +434,120 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
     }
 }
 
+/* The floor of gemm_xres: its grid, segments, barriers and loads (x, the scales, the weights
+ * through two register sets, range ch+2 issued after range ch is used), and no arithmetic but a
+ * checksum: the wrapping sum of every x word as loaded, every scale once and every weight word
+ * once (a clamped or repeated load is not added: a wave past the last row tile, a pair or block
+ * past the row, a scale slot past the segment or the matrix, the re-issue past the last range).
+ * Each workgroup adds its sum to sink[0]. */
+template <int KP, int NW, int SC>
+__global__ __launch_bounds__(64 * NW) void read_xres(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                                     unsigned *sink)
+{
+    constexpr int BS = 2 * KP * SC, XS = 64 * BS, XR = (XS + 64 * NW - 1) / (64 * NW);
+    constexpr int DN = NW * 16 * BS, DR = (DN + 64 * NW - 1) / (64 * NW);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nb = (int)(cols / Q8_BLOCK), np = (nb + 1) / 2;
+    const long tile = blockIdx.x / ks;
+    const int split = (int)(blockIdx.x % ks);
+    const long rt0 = tile * NW + wave;
+    const bool live = rt0 < rows / 16;
+    const int n = lane & 15, kq = lane >> 4;
+    const uint8_t *wt = w + q8s_row_q(live ? rt0 * 16 : 0, cols);
+    const unsigned woff = (unsigned)(n * cols + 16 * kq);
+    unsigned acc = 0;
+    const int r0 = split * cps, nr = (np + KP - 1) / KP;
+    const int mine = nr - r0 < cps ? nr - r0 : cps;
+    for (int sb = 0; sb < mine; sb += SC) {
+        const int nc = mine - sb < SC ? mine - sb : SC;
+        const int c00 = (r0 + sb) * KP, b0 = 2 * c00;
+        uint4 q[2][KP];
+        uint4 xr[XR][2];
+        uint16_t dr[DR];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < XR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k;
+            const int L = s & 63, bs = s >> 6, tok = L & 15;
+            int b = b0 + (bs < BS ? bs : BS - 1);
+            b = b < nb ? b : nb - 1;
+            const float *px = x + (tok < t ? tok : t - 1) * x_stride + (long)b * Q8_BLOCK + kcol(L >> 4);
+            xr[k][0] = *(const uint4 *)px;
+            xr[k][1] = *(const uint4 *)(px + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < DR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k;
+            long row = tile * NW * 16 + s / BS;
+            row = row < rows ? row : rows - 1;
+            int b = b0 + s % BS;
+            b = b < nb ? b : nb - 1;
+            dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int p = 0; p < KP; p++) {
+                int c = c00 + (h < nc ? h : nc - 1) * KP + p;
+                c = c < np ? c : np - 1;
+                q[h][p] = *(const uint4 *)(wt + 64L * c + woff);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < XR; k++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                acc += xr[k][i].x + xr[k][i].y + xr[k][i].z + xr[k][i].w;
+#pragma unroll
+        for (int k = 0; k < DR; k++) {
+            const int s = (int)threadIdx.x + 64 * NW * k, bs = s % BS;
+            if ((DN % (64 * NW) == 0 || s < DN) && tile * NW * 16 + s / BS < rows && bs < 2 * KP * nc && b0 + bs < nb)
+                acc += dr[k];
+        }
+        __syncthreads(); /* where gemm_xres waits for its LDS image */
+#pragma unroll
+        for (int ch = 0; ch < SC; ch++) {
+            if (ch >= nc)
+                break;
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int p = 0; p < KP; p++) {
+                const int c = c00 + ch * KP + p;
+                const uint4 v = q[ch & 1][p];
+                if (live && c < np && 2 * c + (kq >> 1) < nb)
+                    acc += v.x + v.y + v.z + v.w;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (ch + 2 < SC) {
+                const int nx = ch + 2 < nc ? ch + 2 : nc - 1;
+#pragma unroll
+                for (int p = 0; p < KP; p++) {
+                    int c = c00 + nx * KP + p;
+                    c = c < np ? c : np - 1;
+                    q[ch & 1][p] = *(const uint4 *)(wt + 64L * c + woff);
+                }
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        acc += (unsigned)__shfl_xor((int)acc, off, 64);
+    __shared__ unsigned red[NW];
+    if (lane == 0)
+        red[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned v = red[0];
+#pragma unroll
+        for (int k = 1; k < NW; k++)
+            v += red[k];
+        __hip_atomic_fetch_add(sink, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 /* Y = the sum of the ks partials in split order, one thread an output (the kernel boundary
  * before it makes every split's stores visible), plus the residual when res is given (res may be Y) */
 __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *y, const float *res)
@@ -577,6 +691,25 @@ long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o)
 {
     const gemm_plan p = plan_of(rows, cols, t, o);
     return p.ks > 1 ? (long)p.ks * (((t < 64 ? t : 64) + 15) / 16) * 16 * rows : 0;
+}
+
+int q8_launch_read_gemm(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink,
+                        q8_gemm_opts o)
+{
+    if (t < 5 || t > 16)
+        return -1;
+    const gemm_plan p = plan_of(rows, cols, t, o);
+    if (!p.xres)
+        return -1;
+    hipStream_t s = (hipStream_t)stream;
+    const long tiles = (rows + 16L * p.c.nw - 1) / (16L * p.c.nw);
+    if (p.c.nw == 12)
+        Q8_LAUNCH(q8_time_name("read_xres", 3, XRES_KP, 12, XRES_SC), (read_xres<XRES_KP, 12, XRES_SC>), dim3((unsigned)(tiles * p.ks)), dim3(64 * 12), s,
+                  (const uint8_t *)w, rows, cols, x, x_stride, t, p.ks, p.cps, sink);
+    else
+        Q8_LAUNCH(q8_time_name("read_xres", 3, XRES_KP, 16, XRES_SC), (read_xres<XRES_KP, 16, XRES_SC>), dim3((unsigned)(tiles * p.ks)), dim3(64 * 16), s,
+                  (const uint8_t *)w, rows, cols, x, x_stride, t, p.ks, p.cps, sink);
+    return 0;
 }
 
 template <int MG, int RT, int KP, int NW>

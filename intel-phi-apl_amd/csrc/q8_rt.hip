@@ -1175,8 +1175,20 @@ void rt_q8_read_dev(struct rt *R, const void *w0, const void *w1, long rows, lon
         check_shape(c, "rt_q8_read_dev", w1, rows, cols);
     check_dev_ptr("rt_q8_read_dev", x, "x");
     check_dev_ptr("rt_q8_read_dev", sink, "sink");
-    if (t < 1 || t > 4 || (t > 1 && (x_stride < cols || x_stride % 4)))
-        fail("rt_q8_read_dev", "needs 1 to 4 tokens, x rows at least cols floats apart (a multiple of 4)");
+    if (t < 1 || t > 16 || (t > 1 && (x_stride < cols || x_stride % 4)))
+        fail("rt_q8_read_dev", "needs 1 to 16 tokens, x rows at least cols floats apart (a multiple of 4)");
+    if (t >= 5) {
+        if (w1)
+            fail("rt_q8_read_dev", "at 5 to 16 tokens it reads one matrix (the fused pair runs as two products there)");
+        const bool timed = kt_begin(c, RT_K_GEMM, rows, cols, t);
+        if (q8_launch_read_gemm((q8_stream_t)c->stream, w0, rows, cols, x, x_stride, t, sink, c->gemm_opts) != 0) {
+            if (timed)
+                kt_cancel(c);
+            fail("rt_q8_read_dev", "at 5 to 16 tokens it reads for the x-resident matrix-core kernel, which rt_gemm_force has switched off");
+        }
+        launched("the read");
+        return;
+    }
     const bool timed = kt_begin(c, w1 ? RT_K_GEMV_PAIR : RT_K_GEMV, rows, cols, t);
     if (q8_launch_read((q8_stream_t)c->stream, w0, w1, rows, cols, x, x_stride, t, sink) != 0) {
         if (timed)

@@ -770,18 +770,22 @@ def test_c_drop_in_caller(tmp_path):
 
 @pytest.mark.parametrize("rows,cols,pair,t", [(4096, 4096, False, 1), (6144, 4096, False, 1), (4096, 12288, False, 1), (12288, 4096, True, 1),
                                               (3072, 2048, False, 1), (6144, 2048, True, 1), (2048, 6144, False, 1), (151936, 4096, False, 1),
-                                              (12288, 4096, True, 2), (12288, 4096, True, 4), (4096, 12288, False, 3)])
+                                              (12288, 4096, True, 2), (12288, 4096, True, 4), (4096, 12288, False, 3),
+                                              (12288, 4096, False, 16), (4096, 12288, False, 16), (48, 4096, False, 5), (1888, 512, False, 9),
+                                              (64, 1056, False, 7)])
 def test_read_floor_checksum(rt, rows, cols, pair, t):
-    """rt_q8_read_dev (the decode product's loads on its grid at t tokens, no arithmetic: the floor
-    the benchmark sets each product against) reads every byte of the matrix or matrices: its
-    wrapping sum of the 32-bit words read equals numpy's, with x = 0 (each scale is read by two
-    lanes)."""
+    """rt_q8_read_dev (the product's loads on its grid at t tokens, no arithmetic: the floor the
+    benchmark sets each product against) reads every byte of the matrix or matrices: its wrapping
+    sum of the 32-bit words read equals numpy's, with x = 0. At 1 to 4 tokens (the decode kernel)
+    each scale is read by two lanes; at 5 to 16 (the x-resident matrix-core kernel, its K split)
+    each weight word and scale is added once, on partial row tiles (48, 1888 rows) and with a
+    block count that leaves half a pair (1056 columns, 33 blocks) too."""
     rng = np.random.default_rng(rows + cols + pair + 10 * t)
     mats = [synth.q8_rows(rng, rows, cols) for _ in range(2 if pair else 1)]
     want = 0
     for q8 in mats:
         blk = q8.reshape(-1, 34)
-        want += int(blk[:, 2:].copy().view(np.uint32).astype(np.uint64).sum()) + 2 * int(blk[:, :2].copy().view(np.uint16).astype(np.uint64).sum())
+        want += int(blk[:, 2:].copy().view(np.uint32).astype(np.uint64).sum()) + (2 if t <= 4 else 1) * int(blk[:, :2].copy().view(np.uint16).astype(np.uint64).sum())
     ws = [rt.upload(q8, rows, cols) for q8 in mats]
     try:
         with Dev(rt) as d:
