@@ -893,7 +893,10 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
         mg = 1 if name.startswith("gemm_xres") else int(name.split("<")[1].split(",")[0])  # gemm_xres: one token tile
         issued = 2.0 * 3 * (16 * mg * -(-(-(-m // 16)) // mg)) * r_ * c_  # the token tiles the kernel runs: whole groups of MG
         tr = trace.get(key, [])
-        rows.append(f"| {shape} | `{name}` | {mean(tr):.2f} | {k['kernel_us']:.2f} | {k['product_us']:.2f} | {k['GFLOPS']:.0f} | "
+        # the floor (M <= 16): read_xres on the x-resident kernel's grid, from the trace and the bench line
+        fl, ftr = k.get("floor_us"), trace.get((name.replace("gemm_xres", "read_xres"), k["grid"]), [])
+        floor = "—" if fl is None else f"{mean(ftr):.2f} / {fl:.2f}" if ftr else f"— / {fl:.2f}"
+        rows.append(f"| {shape} | `{name}` | {mean(tr):.2f} | {k['kernel_us']:.2f} | {k['product_us']:.2f} | {floor} | {k['GFLOPS']:.0f} | "
                     f"{2.0 * mean(c.get('FETCH_SIZE', [])) * 1024 / 1e6:.1f} | {alg_bytes(r_, c_, m) / 1e6:.1f} | {100 * util:.1f} | "
                     f"{mops * 512 / issued:.3f} | {occupancy_cells(regs, name, *wg_shape.get(key, (0, 64)))} |")
     text = ["# Prompt / verify GEMM on the matrix cores, 9B FFN shapes (rocprofv3)", "",
@@ -901,16 +904,17 @@ def summarize_gemm(run_dir, out=GEMM_PROFILE, xcds=8, simds=1024):
             ">= 512 MB of rotated weight copies. The contraction runs as bf16 MFMA on three exact limbs of x (3x the flops of the "
             "product, tokens padded to 16).", "",
             "Commands (from the repository root; each rocprofv3 run on its own):", "", "```"] + GEMM_PROFILE_CMDS + ["```", "",
-            "| Product | Kernel | Trace avg us | Bench kernel us | Bench product us (with the partial sum) | GFLOP/s (product) | "
-            "HBM MB (FETCH_SIZE x2) | Algorithmic MB | MFMA busy % | counted bf16 MFMA flop / issued | VGPRs a lane | "
-            "Waves a SIMD at most (registers / LDS) |", "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+            "| Product | Kernel | Trace avg us | Bench kernel us | Bench product us (with the partial sum) | Floor us (trace / bench) | "
+            "GFLOP/s (product) | HBM MB (FETCH_SIZE x2) | Algorithmic MB | MFMA busy % | counted bf16 MFMA flop / issued | VGPRs a lane | "
+            "Waves a SIMD at most (registers / LDS) |", "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
     text += rows
     text += ["", f"MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} XCDs x {simds} SIMDs). Counted flop = "
              "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512; issued = 2 x 3 limbs x the token tiles the kernel runs (whole groups of MG "
              "tiles of 16: at M = 40, 4 tiles, one of them all padding) x rows x cols. Counters are per (kernel, grid): "
              "products that launch the same kernel on the same grid share one average. VGPRs a lane from the library's gfx950 "
              "code object; the waves a SIMD they allow (512 registers a lane) and those the workgroup's LDS allows (160 KiB a CU, "
-             "the LDS from the kernel trace), at most 8.", ""]
+             "the LDS from the kernel trace), at most 8. Floor (M = 16): `read_xres`, the x-resident kernel's own loads (x, scales, "
+             "weights through the same two register sets) on its grid with no arithmetic (rt_q8_read_dev at 16 tokens).", ""]
     if stall:
         dh = None
         for l in open(os.path.join(run_dir, "gprof_sq.log")) if os.path.exists(os.path.join(run_dir, "gprof_sq.log")) else []:

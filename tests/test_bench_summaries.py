@@ -82,10 +82,13 @@ def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path, monk
     shapes = {"M16 12288x4096": (xr, 245760, 18.0, 12288, 4096, 16), "M16 4096x12288": (xr, 262144, 19.0, 4096, 12288, 16),
               "M40 12288x4096": (mf, 245760, 27.0, 12288, 4096, 40)}
     line = {"prompt_gemm": {s: {"kernel": n, "grid": g, "kernel_us": us, "product_us": us + 1, "GFLOPS": 1.0} for s, (n, g, us, _, _, _) in shapes.items()}}
+    line["prompt_gemm"]["M16 12288x4096"]["floor_us"] = 14.5
+    line["prompt_gemm"]["M16 4096x12288"]["floor_us"] = 15.25
     os.makedirs(run)
     (run / "gprof_stats.log").write_text(json.dumps(line) + "\n")
-    _trace(str(run / "gprof_stats" / "run_kernel_trace.csv"), [(xr, 245760, [17.0, 17.4]), (xr, 262144, [18.5]), (mf, 245760, [26.0, 28.0])],
-           wg={xr: (115712, 1024), mf: (77824, 1024)})
+    rd = xr.replace("gemm_xres", "read_xres")  # the floor's kernel, on the same grid
+    _trace(str(run / "gprof_stats" / "run_kernel_trace.csv"), [(xr, 245760, [17.0, 17.4]), (xr, 262144, [18.5]), (mf, 245760, [26.0, 28.0]),
+                                                              (rd, 245760, [14.0, 14.2])], wg={xr: (115712, 1024), mf: (77824, 1024)})
     # issued bf16 MFMA flop = 2 x 3 limbs x the token tiles run x rows x cols; the counter counts 512 flop a MOP
     mops = {(n, g): 2.0 * 3 * (16 * (1 if n == xr else 3)) * r * c / 512 for n, g, _, r, c, _ in shapes.values()}
     _counters(str(run / "gprof_fetch" / "run_counter_collection.csv"), [(n, g, "FETCH_SIZE", [30000.0]) for (n, g) in mops])
@@ -101,6 +104,8 @@ def test_gemm_summary_matches_grid_and_counts_the_x_resident_tile(tmp_path, monk
         assert rows[s][-3] == "1.000", s  # counted / issued: one token tile for gemm_xres, three for gemm_mfma<3, ...>
         assert rows[s][-4] == "10.0", s   # MFMA busy: 1024 cycles over (80 / 8 XCDs x 1024 SIMDs)
     assert rows["M16 12288x4096"][-2:] == ["128", "4 / 4"] and rows["M40 12288x4096"][-2:] == ["96", "5 / 8"]
+    # the floor column: trace mean of read_xres on the product's grid / the bench's floor_us; none past M = 16
+    assert rows["M16 12288x4096"][4] == "14.10 / 14.50" and rows["M16 4096x12288"][4] == "— / 15.25" and rows["M40 12288x4096"][4] == "—"
 
 
 def test_gemm_stall_table_by_hand(tmp_path):
