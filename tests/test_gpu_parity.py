@@ -768,6 +768,59 @@ def test_c_drop_in_caller(tmp_path):
     assert p.returncode == 0, p.stdout + p.stderr
 
 
+def _kernels_launched(rt, fn):
+    """(name, grid threads) of the first kernel of every product fn makes, from the runtime's own
+    kernel records (rt_ktime)."""
+    n = 64
+    rt.lib.rt_ktime(rt.R, 1)
+    try:
+        fn()
+        arrs = [np.zeros(n, np.int32), np.zeros(n, np.int64), np.zeros(n, np.int64), np.zeros(n, np.int64), np.zeros(n, np.float32)]
+        names, grid = c.create_string_buffer(64 * n), np.zeros(n, np.int64)
+        got = rt.lib.rt_ktime_read(rt.R, *(a.ctypes.data_as(c.c_void_p) for a in arrs), names, grid.ctypes.data_as(c.c_void_p), n)
+    finally:
+        rt.lib.rt_ktime(rt.R, 0)
+    return [(names.raw[64 * i:64 * i + 64].split(b"\0")[0].decode(), int(grid[i])) for i in range(got)]
+
+
+def _targs(name):
+    return [int(v) for v in name.split("<")[1].rstrip(">").split(",")]
+
+
+@pytest.mark.parametrize("rows,cols,pair,t", [(4096, 4096, False, 1), (4096, 12288, False, 1), (12288, 4096, True, 1), (151936, 4096, False, 1),
+                                              (3072, 2048, False, 1), (12288, 4096, True, 3), (4096, 12288, False, 4), (12288, 4096, False, 16),
+                                              (4096, 12288, False, 16), (6144, 4096, False, 8)])
+def test_read_floor_runs_on_the_products_grid(rt, rows, cols, pair, t):
+    """The floor the benchmark holds a product against is that product's own grid: rt_q8_read_dev
+    launches the read twin of the kernel the product launches (read_k<RW, NW, PAIR, MT> for
+    gemv_k<MT, RW, S, NW, PAIR>, read_xres<KP, NW, SC> for gemm_xres<KP, NW, SC>) with the same
+    number of threads, as the runtime's kernel records show."""
+    rng = np.random.default_rng(rows + cols + t)
+    mats = [synth.q8_rows(rng, rows, cols) for _ in range(2 if pair else 1)]
+    ws = [rt.upload(q8, rows, cols) for q8 in mats]
+    V = c.c_void_p
+    try:
+        with Dev(rt) as d:
+            dx, dy, sink = d.put(np.zeros(t * cols, np.float32)), d.empty(4 * t * rows), d.put(np.zeros(rows, np.uint32))
+            if pair:
+                prod = lambda: rt.lib.rt_gemv_swiglu_dev(rt.R, V(ws[0]), V(ws[1]), rows, cols, V(dx), cols, t, V(dy))  # noqa: E731
+            else:
+                prod = lambda: rt.lib.rt_gemm_dev(rt.R, V(ws[0]), rows, cols, V(dx), cols, t, V(dy))  # noqa: E731
+            (pk, pg), = _kernels_launched(rt, prod)
+            (fk, fg), = _kernels_launched(rt, lambda: rt.lib.rt_q8_read_dev(rt.R, V(ws[0]), V(ws[1]) if pair else None, rows, cols, V(dx), cols, t,
+                                                                             V(sink)))
+    finally:
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, V(w))
+    say("product", pk, pg, "floor", fk, fg)
+    assert fg == pg
+    if t <= 4:
+        mt, rw, s, nw, p = _targs(pk)
+        assert pk.startswith("gemv_k<") and fk == f"read_k<{rw}, {nw}, {p}, {mt}>" and s == 1
+    else:
+        assert pk.startswith("gemm_xres<") and fk == pk.replace("gemm_xres", "read_xres")
+
+
 @pytest.mark.parametrize("rows,cols,pair,t", [(4096, 4096, False, 1), (6144, 4096, False, 1), (4096, 12288, False, 1), (12288, 4096, True, 1),
                                               (3072, 2048, False, 1), (6144, 2048, True, 1), (2048, 6144, False, 1), (151936, 4096, False, 1),
                                               (12288, 4096, True, 2), (12288, 4096, True, 4), (4096, 12288, False, 3),
