@@ -823,7 +823,7 @@ def summarize(run_dir, out=DECODE_PROFILE):
                  f"{roof['bytes_per_launch'] / dt['trace_us'] / 1e3:.1f} GB/s algorithmic = "
                  f"{100 * roof['bytes_per_launch'] / dt['trace_us'] / 1e3 / HBM_PEAK_GBS:.1f} % of {HBM_PEAK_GBS:.0f} GB/s (the unprofiled "
                  "benchmark's events time the same launches; the tracer leaves the GPU idle between dispatches — this run's token took "
-                 f"{line['ms_per_step']} ms with the graph — and a kernel's traced duration runs a few % above what the untraced events measure, so "
+                 f"{line['ms_per_step']} ms with the graph — and a kernel's traced duration runs above what the untraced events measure, the more so the shorter the kernel, so "
                  "this fraction is the conservative one)."]
     text += ["",
              "Machine-readable (read by bench.py for roofline.traffic):", "", "```json", json.dumps(traffic), "```", ""]
