@@ -5,6 +5,7 @@
     the oracle's F32 order bit for bit (1 and 3 tokens);
   - DraftLogits (qwen35.apl:170-172): the first 32768 rows of the same handle equal the first
     32768 outputs of the full product bit for bit;
+  - the 9B model's own 248320 x 4096 output matrix (ref_harness.apl:82-83) at 1 and 4 tokens;
   - the reference keeps gemm(t)[k] == gemv(x[k]) bit for bit (src/card/gemm.h:7). Here the
     reference-order kernel keeps it, the decode kernel (t <= 4) keeps it, and the matrix-core
     product (t >= 5, any K split) does not: its outputs differ from the one-token product's by the
@@ -111,6 +112,26 @@ def test_draft_head_is_prefix(rt, oracle, head, t):
         assert np.array_equal(draft.view(np.uint32), full[:, :DRAFT].view(np.uint32)), f"exact={exact}"
     want = oracle.gemm_f64(head.q8[: DRAFT * HIDDEN // 32 * 34], DRAFT, HIDDEN, x)
     assert_parity(draft, want, f"draft t={t}")
+
+
+MODEL_VOCAB = 248320  # the 9B model's own output matrix (src/apl/ref_harness.apl:82-83)
+
+
+@pytest.mark.parametrize("t", [1, 4])
+def test_model_head_248320_rows(rt, oracle, t):
+    """The 9B model's own output head, 248320 x 4096 (1.08 GB, 31040 workgroups of the decode
+    kernel): the fast kernels at the parity bar against F64 at 1 and 4 tokens, every output finite."""
+    say("model head: drawing 248320 x 4096 Q8_0 on the device")
+    h = Handle(rt, MODEL_VOCAB, HIDDEN, seed=248320 + t)
+    try:
+        x = np.random.default_rng(4000 + t).standard_normal((t, HIDDEN), dtype=np.float32)
+        say(f"model head t={t}: GPU product")
+        y = h.product(x)
+        say(f"model head t={t}: F64 oracle")
+        m = assert_parity(y, oracle.gemm_f64(h.q8, MODEL_VOCAB, HIDDEN, x), f"model head t={t}")
+        say(f"model head t={t}:", m)
+    finally:
+        h.close()
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (4096, 12288)])
