@@ -166,8 +166,11 @@ def test_fast_kernels_on_fixtures(rt, oracle):
         say("fast", case, m)
 
 
-# the configurations' matrices: 2B layer (QKV, out, gate/up, down), 9B layer, and config 1
-SHAPES = [(3072, 2048), (2048, 2048), (6144, 2048), (2048, 6144), (6144, 4096), (4096, 4096), (12288, 4096), (4096, 12288)]
+# the configurations' matrices: 2B layer (QKV, out, gate/up, down), 9B layer, and config 1; then the
+# 9B model's other per-layer matrices (src/apl/qwen35.apl:93-97, 117-120): DeltaNet QKV and attention
+# Q (8192 rows), attention K and V (1024), the DeltaNet beta and alpha (32)
+SHAPES = [(3072, 2048), (2048, 2048), (6144, 2048), (2048, 6144), (6144, 4096), (4096, 4096), (12288, 4096), (4096, 12288),
+          (8192, 4096), (1024, 4096), (32, 4096)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
