@@ -362,14 +362,16 @@ def test_graph_replays_match_eager(rt):
                 rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+@pytest.mark.parametrize("shapes", [[8192, 4096, 32, 32], [8192, 1024, 1024]], ids=["deltanet_quartet", "attention_qkv"])
 @pytest.mark.parametrize("t", [1, 3])
-def test_round_one_launch_equals_singles(rt, oracle, t):
+def test_round_one_launch_equals_singles(rt, oracle, t, shapes):
     """The 9B DeltaNet quartet (QKV 8192x4096, GATE 4096x4096, BETA and ALPHA 32x4096, all reading H;
-    src/apl/qwen35.apl:93-96) as one launch (rt_gemv_round_dev) gives each product's bits as its own
-    launch does, and meets the parity bar."""
+    src/apl/qwen35.apl:93-96) and the attention layer's Q, K and V (8192, 1024 and 1024 x 4096;
+    qwen35.apl:117-119) as one launch (rt_gemv_round_dev) give each product's bits as its own
+    launch does, and meet the parity bar."""
     cols = 4096
-    shapes = [8192, 4096, 32, 32]
-    rng = np.random.default_rng(60 + t)
+    n = len(shapes)
+    rng = np.random.default_rng(60 + t + n)
     mats = [synth.q8_rows(rng, r, cols) for r in shapes]
     x = synth.x_f32(rng, t, cols)
     ws = [rt.upload(m, r, cols) for m, r in zip(mats, shapes)]
@@ -378,10 +380,10 @@ def test_round_one_launch_equals_singles(rt, oracle, t):
         with Dev(rt) as d:
             dx = d.put(x)
             ys = [d.empty(4 * t * r) for r in shapes]
-            W = (c.c_void_p * 4)(*ws)
-            R = (c.c_long * 4)(*shapes)
-            Y = (c.c_void_p * 4)(*ys)
-            rt.lib.rt_gemv_round_dev(rt.R, 4, W, R, cols, c.c_void_p(dx), cols, t, Y)
+            W = (c.c_void_p * n)(*ws)
+            R = (c.c_long * n)(*shapes)
+            Y = (c.c_void_p * n)(*ys)
+            rt.lib.rt_gemv_round_dev(rt.R, n, W, R, cols, c.c_void_p(dx), cols, t, Y)
             got = [d.get(p, (t, r), np.float32) for p, r in zip(ys, shapes)]
         for g, s1, m, r in zip(got, singles, mats, shapes):
             assert np.array_equal(g.view(np.uint32), s1.view(np.uint32)), r
