@@ -422,6 +422,52 @@ def deltanet_round(b):
     return out
 
 
+def prompt_rounds(b):
+    """At M = 16 tokens (a prompt chunk, a speculative verify), three rounds of products that share x,
+    over 32 layers of distinct weights, each recorded as a graph: every product launched alone (its
+    matrix-core kernel and its partial sum) against one round a layer (rt_gemv_round_dev: one
+    x-resident launch for the products of each wave count, one launch of the sums). The 9B DeltaNet
+    quartet (qwen35.apl:93-96), the attention layer's Q, K and V (qwen35.apl:117-119) and the FFN's
+    gate and up (12288 x 4096 each). GB/s counts the weights' bytes."""
+    m, out = 16, {}
+    for name, shapes in (("deltanet_quartet", [8192, 4096, 32, 32]), ("attention_qkv", [8192, 1024, 1024]), ("ffn_gate_up", [FFN, FFN])):
+        n = len(shapes)
+        layers = [[b.matrix(r, HIDDEN) for r in shapes] for _ in range(LAYERS)]
+        x, ys = b.vec(m * HIDDEN), [b.vec(m * r) for r in shapes]
+        R, Y = (c.c_long * n)(*shapes), (c.c_void_p * n)(*ys)
+        Ws = [(c.c_void_p * n)(*L) for L in layers]
+        per = LAYERS * sum(q8_bytes(r, HIDDEN) for r in shapes)
+
+        def singles():
+            for L in layers:
+                for w, r, y in zip(L, shapes, ys):
+                    b.gemm(w, r, HIDDEN, x, m, y)
+
+        def rounds():
+            for W in Ws:
+                b.lib.rt_gemv_round_dev(b.R, n, W, R, HIDDEN, c.c_void_p(x), HIDDEN, m, Y)
+
+        res = {"weight_bytes": per}
+        for key, fn in (("products_alone", singles), ("one_round", rounds)):
+            fn()  # eager first: the workspace is allocated before the graph records
+            b.rt.sync()
+            b.lib.rt_graph_begin(b.R)
+            fn()
+            g = b.lib.rt_graph_end(b.R)
+            b.lib.rt_graph_launch(b.R, c.c_void_p(g))
+            ms = b.timed(lambda: b.lib.rt_graph_launch(b.R, c.c_void_p(g)), 10)
+            b.lib.rt_graph_free(b.R, c.c_void_p(g))
+            res[key] = {"us_per_layer": round(1e3 * ms / LAYERS, 2), "GB/s": round(per / ms / 1e6, 1)}
+        for L in layers:
+            for w in L:
+                b.rt.free(w)
+        b.rt.free(x)
+        for y in ys:
+            b.rt.free(y)
+        out[name] = res
+    return out
+
+
 HOSTBENCH = os.path.join(ROOT, "intel-phi-apl_amd", "q8_hostbench")
 
 
@@ -1184,7 +1230,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", metavar="SECTIONS", help="comma-separated sections to run instead of the full line (gemv_4096x4096, "
-                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, host_pointers, gguf_load_9b_layer, "
+                    "draft_head, prompt_gemm, verify, 2b_layer_set, deltanet_round_9b, prompt_rounds_9b, host_pointers, gguf_load_9b_layer, "
                     "epilogues_9b); prints their results only")
     ap.add_argument("--summarize", metavar="DIR", help="write the rocprofv3 summary under profiles/ from DIR (the output of the "
                     "profile commands) and exit")
@@ -1212,7 +1258,7 @@ def main():
               "shard by whole 16-row groups, each GPU computing its slice of y)", file=sys.stderr)
         sys.exit(2)
     sections = (("gemv_4096x4096", single_gemv), ("draft_head", draft_head), ("prompt_gemm", prompt_gemm), ("verify", verify_path),
-                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round),
+                ("2b_layer_set", layers_2b), ("deltanet_round_9b", deltanet_round), ("prompt_rounds_9b", prompt_rounds),
                 ("gguf_load_9b_layer", gguf_load), ("epilogues_9b", epilogues_9b))
     if a.only:
         sections = sections + (("token_trace", token_trace),)

@@ -277,10 +277,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
  * barrier; then each wave streams its weights through two register sets (range ch+1's loads in
  * flight during range ch's MFMAs) with no further synchronisation. gemm_mfma instead loads x and
  * the scales for every range, and waits for them and for a barrier before each range's MFMAs.
- * The sums are gemm_mfma's in the same order, so on the same split the two give the same bits. */
+ * The sums are gemm_mfma's in the same order, so on the same split the two give the same bits.
+ * blk: the workgroup's index in the product's grid (tile blk / ks, split blk % ks). */
 template <int KP, int NW, int SC>
-__global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
-                                                     float *part, float *y, const float *res)
+__device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                          float *part, float *y, const float *res, unsigned blk)
 {
     constexpr int BS = 2 * KP * SC;                     /* blocks of a segment */
     constexpr int XS = 64 * BS;                         /* x lane slots of a segment: 8 values of one token */
@@ -296,8 +297,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     /* block, pair and range indices in 32 bits: gfx9 compares 64-bit values only in vector registers */
     const int nb = (int)(cols / Q8_BLOCK), np = (nb + 1) / 2;
-    const long tile = blockIdx.x / ks;
-    const int split = (int)(blockIdx.x % ks);
+    const long tile = blk / ks;
+    const int split = (int)(blk % ks);
     const long rt0 = tile * NW + wave;
     /* a wave past the last row tile reads row tile 0 and contributes nothing */
     const bool live = rt0 < rows / 16;
@@ -434,6 +435,28 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
     }
 }
 
+template <int KP, int NW, int SC>
+__global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                                     float *part, float *y, const float *res)
+{
+    xres_body<KP, NW, SC>(w, rows, cols, x, x_stride, t, ks, cps, part, y, res, blockIdx.x);
+}
+
+/* A round of products that share x (and t <= 16) as one launch: workgroup b belongs to product p
+ * with start[p] <= b < start[p+1] and runs that product's own grid position b - start[p] on its
+ * own plan, so every product gets the bits of its own launch. */
+template <int KP, int NW, int SC>
+__global__ __launch_bounds__(64 * NW) void gemm_xres_round(q8_gemm_round r, long cols, const float *x, long x_stride, long t)
+{
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < Q8_ROUND_MAX; k++)
+        if (k < r.n && (long)blockIdx.x >= r.start[k])
+            p = k;
+    xres_body<KP, NW, SC>((const uint8_t *)r.w[p], r.rows[p], cols, x, x_stride, t, r.ks[p], r.cps[p], r.out[p], r.out[p], nullptr,
+                          (unsigned)(blockIdx.x - r.start[p]));
+}
+
 /* The floor of gemm_xres: its grid, segments, barriers and loads (x, the scales, the weights
  * through two register sets, range ch+2 issued after range ch is used), and no arithmetic but a
  * checksum: the wrapping sum of every x word as loaded, every scale once and every weight word
@@ -548,17 +571,11 @@ __global__ __launch_bounds__(64 * NW) void read_xres(const uint8_t *w, long rows
     }
 }
 
-/* Y = the sum of the ks partials in split order, one thread an output (the kernel boundary
- * before it makes every split's stores visible), plus the residual when res is given (res may be Y) */
-__global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *y, const float *res)
+/* output i's sum of the ks partials (splits step floats apart), in split order: sixteen splits'
+ * loads in flight at a time, all issued before the first add (past the last split the index is
+ * clamped and the value not added) */
+__device__ __forceinline__ float split_sum(const float *__restrict__ part, int ks, long step, long i)
 {
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= t * rows)
-        return;
-    const long step = tp * rows;
-    const float r = res ? res[i] : 0.0f;
-    /* sixteen splits' loads in flight at a time, all issued before the first add (past the last
-     * split the index is clamped and the value not added); added in split order */
     float v = 0.0f;
     for (int s0 = 0; s0 < ks; s0 += 16) {
         float a[16];
@@ -570,7 +587,35 @@ __global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, 
             if (s0 + k < ks)
                 v = s0 + k == 0 ? a[0] : v + a[k];
     }
+    return v;
+}
+
+/* Y = the sum of the ks partials in split order, one thread an output (the kernel boundary
+ * before it makes every split's stores visible), plus the residual when res is given (res may be Y) */
+__global__ __launch_bounds__(256) void gemm_sum(const float *__restrict__ part, int ks, long t, long tp, long rows, float *y, const float *res)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= t * rows)
+        return;
+    const float r = res ? res[i] : 0.0f;
+    const float v = split_sum(part, ks, tp * rows, i);
     y[i] = res ? r + v : v;
+}
+
+/* the sums of a round's products: output i of the round belongs to product p with ostart[p] <= i <
+ * ostart[p+1]; a product of one split wrote its Y itself */
+__global__ __launch_bounds__(256) void gemm_sum_round(q8_gemm_round r, long tp)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < Q8_ROUND_MAX; k++)
+        if (k < r.n && i >= r.ostart[k])
+            p = k;
+    if (i >= r.ostart[r.n] || r.ks[p] == 1)
+        return;
+    const long j = i - r.ostart[p];
+    r.y[p][j] = split_sum(r.out[p], r.ks[p], tp * r.rows[p], j);
 }
 
 /* ---------------------------------------------------------------- launchers */
@@ -691,6 +736,72 @@ long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o)
 {
     const gemm_plan p = plan_of(rows, cols, t, o);
     return p.ks > 1 ? (long)p.ks * (((t < 64 ? t : 64) + 15) / 16) * 16 * rows : 0;
+}
+
+int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
+                         float *const *y, float *part, q8_gemm_opts o)
+{
+    if (t < 5 || t > 16 || n < 2 || n > Q8_ROUND_MAX)
+        return -1;
+    /* every product's plan, partials and outputs, in the round's order */
+    q8_gemm_round all{};
+    all.n = n;
+    int nws[Q8_ROUND_MAX];
+    const long tp = 16;
+    long parts = 0, outs = 0;
+    for (int p = 0; p < n; p++) {
+        const gemm_plan pl = plan_of(rows[p], cols, t, o);
+        if (!pl.xres)
+            return -1;
+        nws[p] = pl.c.nw;
+        all.w[p] = w[p];
+        all.rows[p] = rows[p];
+        all.ks[p] = pl.ks;
+        all.cps[p] = pl.cps;
+        all.y[p] = y[p];
+        all.ostart[p] = outs;
+        outs += t * rows[p];
+        if (pl.ks > 1) {
+            all.out[p] = part + parts;
+            parts += (long)pl.ks * tp * rows[p];
+        } else {
+            all.out[p] = y[p];
+        }
+    }
+    all.ostart[n] = outs;
+    if (parts > Q8_GEMM_PART_MAX || (parts > 0 && !part))
+        return -1;
+    hipStream_t s = (hipStream_t)stream;
+    /* one x-resident launch for the products of each wave count, then every product's sums */
+    for (int nw : {16, 12}) {
+        q8_gemm_round g{};
+        long wgs = 0;
+        for (int p = 0; p < n; p++) {
+            if (nws[p] != nw)
+                continue;
+            const int k = g.n++;
+            g.w[k] = all.w[p];
+            g.rows[k] = all.rows[p];
+            g.ks[k] = all.ks[p];
+            g.cps[k] = all.cps[p];
+            g.out[k] = all.out[p];
+            g.y[k] = all.y[p];
+            g.start[k] = wgs;
+            wgs += (rows[p] + 16L * nw - 1) / (16L * nw) * all.ks[p];
+        }
+        if (!g.n)
+            continue;
+        g.start[g.n] = wgs;
+        if (nw == 12)
+            Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 12, XRES_SC), (gemm_xres_round<XRES_KP, 12, XRES_SC>), dim3((unsigned)wgs),
+                      dim3(64 * 12), s, g, cols, x, x_stride, t);
+        else
+            Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 16, XRES_SC), (gemm_xres_round<XRES_KP, 16, XRES_SC>), dim3((unsigned)wgs),
+                      dim3(64 * 16), s, g, cols, x, x_stride, t);
+    }
+    if (parts > 0)
+        gemm_sum_round<<<dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s>>>(all, tp);
+    return 0;
 }
 
 int q8_launch_read_gemm(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, unsigned *sink,

@@ -412,8 +412,10 @@ void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, c
     launched("the residual add");
 }
 
-/* Products sharing x as one launch: true when launched, false when the kernel does not take the
- * shape (the caller then runs them one by one). */
+/* Products sharing x as one launch: at t <= 4 the decode round, at 5 <= t <= 16 the x-resident
+ * matrix-core round (each product on its own plan, so with its own launch's bits) and one launch
+ * of their partial sums. True when launched, false when the kernels do not take the shapes (the
+ * caller then runs them one by one). */
 bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long cols, const float *x, long xs, long t, float *const *y)
 {
     const bool timed = c->ktime_on && c->kt.size() < KT_MAX;
@@ -425,7 +427,20 @@ bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long co
         c->kt.push_back(ktrec{RT_K_ROUND, total, cols, t, 0, {0}});
         q8_time_next(c->kt_events[2 * k], c->kt_events[2 * k + 1], c->kt.back().name, &c->kt.back().grid);
     }
-    if (q8_launch_gemv_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y) != 0) {
+    int rc;
+    if (t <= 4) {
+        rc = q8_launch_gemv_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y);
+    } else {
+        bool parts = false;
+        for (int i = 0; i < n; i++)
+            parts = parts || q8_gemm_part_floats(rows[i], cols, t, c->gemm_opts) > 0;
+        if (parts && !c->part) {
+            no_capture(c, "the matrix-core product's partial sums");
+            HIPCHECK(hipMalloc((void **)&c->part, (size_t)Q8_GEMM_PART_MAX * sizeof(float)));
+        }
+        rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y, c->part, c->gemm_opts);
+    }
+    if (rc != 0) {
         if (timed) {
             q8_time_next(nullptr, nullptr, nullptr, nullptr);
             c->kt.pop_back();
@@ -523,10 +538,10 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
         q8_launch_copy((q8_stream_t)c->stream, c->dx, c->hx, (long)(nx / 4)); /* nx is a multiple of 64 floats */
         launched("the copy of x");
     }
-    /* decode products that share x (and t): one launch for the group */
+    /* products that share x (and t <= 16): one round for the group */
     bool done[RT_BATCH] = {};
     for (int i = 0; i < n && !c->exact; i++) {
-        if (done[i] || jobs[i].t > 4)
+        if (done[i] || jobs[i].t > 16)
             continue;
         const void *w[RT_BATCH];
         long rows[RT_BATCH];
@@ -905,7 +920,7 @@ void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *ro
         check_shape(c, "rt_gemv_round_dev", w[i], rows[i], cols);
         check_dev_ptr("rt_gemv_round_dev", y[i], "every y");
     }
-    if (!c->exact && t <= 4 && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
+    if (!c->exact && t <= 16 && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
         return;
     for (int i = 0; i < n; i++)
         product(c, w[i], nullptr, rows[i], cols, x, x_stride, t, y[i]);
@@ -995,7 +1010,7 @@ void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const lon
     float *xn = reserve_epi(c, (size_t)(t * cols));
     q8_launch_rmsnorm(s, x, x_stride, t, cols, nw, eps, xn);
     launched("the norm");
-    if (!c->exact && t <= 4 && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
+    if (!c->exact && t <= 16 && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
         return;
     for (int i = 0; i < n; i++)
         product(c, w[i], nullptr, rows[i], cols, xn, cols, t, y[i]);
