@@ -423,14 +423,16 @@ def deltanet_round(b):
 
 
 def prompt_rounds(b):
-    """At M = 16 tokens (a prompt chunk, a speculative verify), three rounds of products that share x,
-    over 32 layers of distinct weights, each recorded as a graph: every product launched alone (its
-    matrix-core kernel and its partial sum) against one round a layer (rt_gemv_round_dev: one
-    x-resident launch for the products of each wave count, one launch of the sums). The 9B DeltaNet
-    quartet (qwen35.apl:93-96), the attention layer's Q, K and V (qwen35.apl:117-119) and the FFN's
-    gate and up (12288 x 4096 each). GB/s counts the weights' bytes."""
-    m, out = 16, {}
-    for name, shapes in (("deltanet_quartet", [8192, 4096, 32, 32]), ("attention_qkv", [8192, 1024, 1024]), ("ffn_gate_up", [FFN, FFN])):
+    """At M = 16 and 64 tokens (a prompt chunk, a speculative verify), three rounds of products that
+    share x, over 32 layers of distinct weights, each recorded as a graph: every product launched
+    alone (its matrix-core kernel and its partial sum) against one round a layer
+    (rt_gemv_round_dev: one launch for the products of each kernel configuration, one launch of the
+    sums). The 9B DeltaNet quartet (qwen35.apl:93-96), the attention layer's Q, K and V
+    (qwen35.apl:117-119) and the FFN's gate and up (12288 x 4096 each). GB/s counts the weights'
+    bytes."""
+    out = {}
+    for m, name, shapes in [(m, name, shapes) for m in (16, 64) for name, shapes in
+                            (("deltanet_quartet", [8192, 4096, 32, 32]), ("attention_qkv", [8192, 1024, 1024]), ("ffn_gate_up", [FFN, FFN]))]:
         n = len(shapes)
         layers = [[b.matrix(r, HIDDEN) for r in shapes] for _ in range(LAYERS)]
         x, ys = b.vec(m * HIDDEN), [b.vec(m * r) for r in shapes]
@@ -464,7 +466,7 @@ def prompt_rounds(b):
         b.rt.free(x)
         for y in ys:
             b.rt.free(y)
-        out[name] = res
+        out[f"M{m} {name}"] = res
     return out
 
 

@@ -255,11 +255,11 @@ struct q8_gemm_opts {
 void q8_launch_gemm_mfma(q8_stream_t stream, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y, float *part,
                          const float *res, q8_gemm_opts o);
 long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o);
-/* A round of products sharing x at 5 <= t <= 16 tokens: one x-resident launch for the products of
- * each wave count (16, 12) and one launch of every product's partial sums, each product on its own
- * plan (its single launch's bits): 0, or -1 (nothing launched: a product's plan is not
- * x-resident, or the partials exceed Q8_GEMM_PART_MAX floats of part; the caller runs them one
- * by one). */
+/* A round of products sharing x at 5 <= t <= 64 tokens: one matrix-core launch for the products of
+ * each kernel configuration (at t <= 16 the x-resident kernel's wave count, above it the streaming
+ * kernel's) and one launch of every product's partial sums, each product on its own plan (its
+ * single launch's bits): 0, or -1 (nothing launched: the partials need more than part_cap floats
+ * of part, q8_gemm_round_part_floats; the caller runs them one by one). */
 struct q8_gemm_round {
     int n;
     const void *w[Q8_ROUND_MAX];
@@ -271,7 +271,8 @@ struct q8_gemm_round {
     long ostart[Q8_ROUND_MAX + 1]; /* first output (t x rows a product); ostart[n] = the outputs */
 };
 int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
-                         float *const *y, float *part, q8_gemm_opts o);
+                         float *const *y, float *part, long part_cap, q8_gemm_opts o);
+long q8_gemm_round_part_floats(int n, const long *rows, long cols, long t, q8_gemm_opts o);
 /* The floor of the x-resident product at 5 <= t <= 16 tokens: its loads on its grid (the plan for
  * these options), no arithmetic, a checksum added to sink[0]; -1 when the plan is not the
  * x-resident kernel. */

@@ -74,10 +74,11 @@ struct gemm_stage {
  * issued at once: a memory-bound kernel is as fast as the bytes it keeps in flight. The ranges
  * are software-pipelined: the loads of range ch+1 are issued into a second register set before
  * the MFMAs of range ch, so a workgroup streams its K slice with one range always in flight.
- * The ks workgroups of a row tile write partials that gemm_sum adds in split order. */
+ * The ks workgroups of a row tile write partials that gemm_sum adds in split order. blk: the
+ * workgroup's index in the product's grid along x (tile blk / ks, split blk % ks). */
 template <int MT, int RT, int KP, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
-                                                     float *part, float *y, const float *res)
+__device__ __forceinline__ void mfma_body(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                          float *part, float *y, const float *res, unsigned blk)
 {
     typedef gemm_stage<MT, RT, KP, NW> stage;
     constexpr int XS = stage::XS, XR = stage::XR, DN = stage::DN, DR = stage::DR;
@@ -89,8 +90,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     /* block, pair and range indices in 32 bits (see gemm_xres) */
     const int nb = (int)(cols / Q8_BLOCK), np = (nb + 1) / 2;
-    const long tile = blockIdx.x / ks;
-    const int split = (int)(blockIdx.x % ks);
+    const long tile = blk / ks;
+    const int split = (int)(blk % ks);
     const long tt0 = (long)blockIdx.y * MT;
     const long rt0 = (tile * NW + wave) * RT;
     /* a row tile past the last one (of a wave's RT, any but the first may be) reads row tile 0
@@ -268,6 +269,27 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
                 }
             }
     }
+}
+
+template <int MT, int RT, int KP, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
+                                                     float *part, float *y, const float *res)
+{
+    mfma_body<MT, RT, KP, NW>(w, rows, cols, x, x_stride, t, ks, cps, part, y, res, blockIdx.x);
+}
+
+/* A round of products sharing x (17 <= t <= 64) of one configuration as one launch: workgroup
+ * (b, g) runs position (b - start[p], g) of product p's own grid on its own plan */
+template <int MT, int RT, int KP, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_mfma_round(q8_gemm_round r, long cols, const float *x, long x_stride, long t)
+{
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < Q8_ROUND_MAX; k++)
+        if (k < r.n && (long)blockIdx.x >= r.start[k])
+            p = k;
+    mfma_body<MT, RT, KP, NW>((const uint8_t *)r.w[p], r.rows[p], cols, x, x_stride, t, r.ks[p], r.cps[p], r.out[p], r.out[p], nullptr,
+                              (unsigned)(blockIdx.x - r.start[p]));
 }
 
 /* One token tile (t <= 16) with x resident in LDS. A workgroup of NW waves owns NW row tiles
@@ -738,47 +760,73 @@ long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o)
     return p.ks > 1 ? (long)p.ks * (((t < 64 ? t : 64) + 15) / 16) * 16 * rows : 0;
 }
 
-int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
-                         float *const *y, float *part, q8_gemm_opts o)
+/* a round's products: plans, partial regions (from part, or null to count), outputs; the floats of
+ * partials it needs in *parts */
+static void round_plan(int n, const void *const *w, const long *rows, long cols, long t, float *const *y, float *part, q8_gemm_opts o,
+                       q8_gemm_round &all, gemm_plan *pl, long *parts)
 {
-    if (t < 5 || t > 16 || n < 2 || n > Q8_ROUND_MAX)
-        return -1;
-    /* every product's plan, partials and outputs, in the round's order */
-    q8_gemm_round all{};
+    const long tp = (t + 15) / 16 * 16;
+    long np = 0, outs = 0;
+    all = q8_gemm_round{};
     all.n = n;
-    int nws[Q8_ROUND_MAX];
-    const long tp = 16;
-    long parts = 0, outs = 0;
     for (int p = 0; p < n; p++) {
-        const gemm_plan pl = plan_of(rows[p], cols, t, o);
-        if (!pl.xres)
-            return -1;
-        nws[p] = pl.c.nw;
-        all.w[p] = w[p];
+        pl[p] = plan_of(rows[p], cols, t, o);
+        all.w[p] = w ? w[p] : nullptr;
         all.rows[p] = rows[p];
-        all.ks[p] = pl.ks;
-        all.cps[p] = pl.cps;
-        all.y[p] = y[p];
+        all.ks[p] = pl[p].ks;
+        all.cps[p] = pl[p].cps;
+        all.y[p] = y ? y[p] : nullptr;
         all.ostart[p] = outs;
         outs += t * rows[p];
-        if (pl.ks > 1) {
-            all.out[p] = part + parts;
-            parts += (long)pl.ks * tp * rows[p];
+        if (pl[p].ks > 1) {
+            all.out[p] = part ? part + np : nullptr;
+            np += (long)pl[p].ks * tp * rows[p];
         } else {
-            all.out[p] = y[p];
+            all.out[p] = all.y[p];
         }
     }
     all.ostart[n] = outs;
-    if (parts > Q8_GEMM_PART_MAX || (parts > 0 && !part))
+    *parts = np;
+}
+
+long q8_gemm_round_part_floats(int n, const long *rows, long cols, long t, q8_gemm_opts o)
+{
+    if (t < 5 || t > 64 || n < 2 || n > Q8_ROUND_MAX)
+        return 0;
+    q8_gemm_round all;
+    gemm_plan pl[Q8_ROUND_MAX];
+    long parts = 0;
+    round_plan(n, nullptr, rows, cols, t, nullptr, nullptr, o, all, pl, &parts);
+    return parts;
+}
+
+int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
+                         float *const *y, float *part, long part_cap, q8_gemm_opts o)
+{
+    if (t < 5 || t > 64 || n < 2 || n > Q8_ROUND_MAX)
+        return -1;
+    q8_gemm_round all;
+    gemm_plan pl[Q8_ROUND_MAX];
+    long parts = 0;
+    round_plan(n, w, rows, cols, t, y, part, o, all, pl, &parts);
+    if (parts > part_cap || (parts > 0 && !part))
         return -1;
     hipStream_t s = (hipStream_t)stream;
-    /* one x-resident launch for the products of each wave count, then every product's sums */
-    for (int nw : {16, 12}) {
+    /* one launch for the products of each kernel configuration (the x-resident kernel's wave count,
+     * or the streaming kernel's MG, RT, KP, NW), then every product's sums */
+    bool launched[Q8_ROUND_MAX] = {};
+    for (int p0 = 0; p0 < n; p0++) {
+        if (launched[p0])
+            continue;
+        const gemm_plan &c0 = pl[p0];
+        const int rowsper = 16 * c0.c.nw * (c0.xres ? 1 : c0.c.rt);
         q8_gemm_round g{};
         long wgs = 0;
-        for (int p = 0; p < n; p++) {
-            if (nws[p] != nw)
+        for (int p = p0; p < n; p++) {
+            if (launched[p] || pl[p].xres != c0.xres || pl[p].c.nw != c0.c.nw ||
+                (!c0.xres && (pl[p].c.mg != c0.c.mg || pl[p].c.rt != c0.c.rt || pl[p].c.kp != c0.c.kp)))
                 continue;
+            launched[p] = true;
             const int k = g.n++;
             g.w[k] = all.w[p];
             g.rows[k] = all.rows[p];
@@ -787,20 +835,36 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
             g.out[k] = all.out[p];
             g.y[k] = all.y[p];
             g.start[k] = wgs;
-            wgs += (rows[p] + 16L * nw - 1) / (16L * nw) * all.ks[p];
+            wgs += (rows[p] + rowsper - 1) / rowsper * all.ks[p];
         }
-        if (!g.n)
-            continue;
         g.start[g.n] = wgs;
-        if (nw == 12)
-            Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 12, XRES_SC), (gemm_xres_round<XRES_KP, 12, XRES_SC>), dim3((unsigned)wgs),
-                      dim3(64 * 12), s, g, cols, x, x_stride, t);
-        else
-            Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 16, XRES_SC), (gemm_xres_round<XRES_KP, 16, XRES_SC>), dim3((unsigned)wgs),
-                      dim3(64 * 16), s, g, cols, x, x_stride, t);
+        bool ok = false;
+        if (c0.xres) {
+            if (c0.c.nw == 12)
+                Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 12, XRES_SC), (gemm_xres_round<XRES_KP, 12, XRES_SC>), dim3((unsigned)wgs),
+                          dim3(64 * 12), s, g, cols, x, x_stride, t);
+            else
+                Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 16, XRES_SC), (gemm_xres_round<XRES_KP, 16, XRES_SC>), dim3((unsigned)wgs),
+                          dim3(64 * 16), s, g, cols, x, x_stride, t);
+            ok = true;
+        } else {
+            const unsigned groups = (unsigned)(((t + 15) / 16 + c0.c.mg - 1) / c0.c.mg);
+#define GR(G, R, P, N)                                                                                                 \
+    if (!ok && c0.c.mg == G && c0.c.rt == R && c0.c.kp == P && c0.c.nw == N) {                                         \
+        Q8_LAUNCH(q8_time_name("gemm_mfma_round", 4, G, R, P, N), (gemm_mfma_round<G, R, P, N>), dim3((unsigned)wgs, groups), dim3(64 * N), s, g,    \
+                  cols, x, x_stride, t);                                                                               \
+        ok = true;                                                                                                     \
+    }
+            GEMM_CFGS(GR)
+#undef GR
+        }
+        if (!ok) {
+            fprintf(stderr, "q8_gemm: no round kernel for MG %d RT %d KP %d NW %d\n", c0.c.mg, c0.c.rt, c0.c.kp, c0.c.nw);
+            abort();
+        }
     }
     if (parts > 0)
-        gemm_sum_round<<<dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s>>>(all, tp);
+        gemm_sum_round<<<dim3((unsigned)((all.ostart[n] + 255) / 256)), dim3(256), 0, s>>>(all, (t + 15) / 16 * 16);
     return 0;
 }
 

@@ -113,6 +113,9 @@ struct ctx {
     size_t epi_cap = 0;
     /* the matrix-core product's K-split partials */
     float *part = nullptr;
+    /* a matrix-core round's partials, every product's */
+    float *rpart = nullptr;
+    size_t rpart_cap = 0;
     /* the device address of `scratch` on this runtime's GPU (rt_gemm_dev_noalloc's partials) */
     float *noalloc_part = nullptr;
     /* the greedy next token's candidates */
@@ -412,10 +415,11 @@ void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, c
     launched("the residual add");
 }
 
-/* Products sharing x as one launch: at t <= 4 the decode round, at 5 <= t <= 16 the x-resident
- * matrix-core round (each product on its own plan, so with its own launch's bits) and one launch
- * of their partial sums. True when launched, false when the kernels do not take the shapes (the
- * caller then runs them one by one). */
+/* Products sharing x as one launch: at t <= 4 the decode round, at 5 <= t <= 64 the matrix-core
+ * round (one launch a kernel configuration, each product on its own plan, so with its own
+ * launch's bits) and one launch of their partial sums, in a workspace of its own grown to the
+ * round. True when launched, false when the kernels do not take the shapes (the caller then runs
+ * them one by one). */
 bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long cols, const float *x, long xs, long t, float *const *y)
 {
     const bool timed = c->ktime_on && c->kt.size() < KT_MAX;
@@ -431,14 +435,15 @@ bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long co
     if (t <= 4) {
         rc = q8_launch_gemv_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y);
     } else {
-        bool parts = false;
-        for (int i = 0; i < n; i++)
-            parts = parts || q8_gemm_part_floats(rows[i], cols, t, c->gemm_opts) > 0;
-        if (parts && !c->part) {
-            no_capture(c, "the matrix-core product's partial sums");
-            HIPCHECK(hipMalloc((void **)&c->part, (size_t)Q8_GEMM_PART_MAX * sizeof(float)));
+        const size_t need = (size_t)q8_gemm_round_part_floats(n, rows, cols, t, c->gemm_opts);
+        if (need > c->rpart_cap) {
+            no_capture(c, "a matrix-core round's partial sums");
+            if (c->rpart)
+                c->retired.push_back(c->rpart);
+            HIPCHECK(hipMalloc((void **)&c->rpart, need * sizeof(float)));
+            c->rpart_cap = need;
         }
-        rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y, c->part, c->gemm_opts);
+        rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y, c->rpart, (long)c->rpart_cap, c->gemm_opts);
     }
     if (rc != 0) {
         if (timed) {
@@ -538,10 +543,10 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
         q8_launch_copy((q8_stream_t)c->stream, c->dx, c->hx, (long)(nx / 4)); /* nx is a multiple of 64 floats */
         launched("the copy of x");
     }
-    /* products that share x (and t <= 16): one round for the group */
+    /* products that share x (and t <= 64): one round for the group */
     bool done[RT_BATCH] = {};
     for (int i = 0; i < n && !c->exact; i++) {
-        if (done[i] || jobs[i].t > 16)
+        if (done[i] || jobs[i].t > 64)
             continue;
         const void *w[RT_BATCH];
         long rows[RT_BATCH];
@@ -652,6 +657,8 @@ void rt_fini(struct rt *R)
         HIPCHECK(hipFree(c->part));
     if (c->epi)
         HIPCHECK(hipFree(c->epi));
+    if (c->rpart)
+        HIPCHECK(hipFree(c->rpart));
     for (void *p : c->retired)
         HIPCHECK(hipFree(p));
     for (auto &e : c->kt_events)
@@ -920,7 +927,7 @@ void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *ro
         check_shape(c, "rt_gemv_round_dev", w[i], rows[i], cols);
         check_dev_ptr("rt_gemv_round_dev", y[i], "every y");
     }
-    if (!c->exact && t <= 16 && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
+    if (!c->exact && t <= 64 && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
         return;
     for (int i = 0; i < n; i++)
         product(c, w[i], nullptr, rows[i], cols, x, x_stride, t, y[i]);
@@ -1010,7 +1017,7 @@ void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const lon
     float *xn = reserve_epi(c, (size_t)(t * cols));
     q8_launch_rmsnorm(s, x, x_stride, t, cols, nw, eps, xn);
     launched("the norm");
-    if (!c->exact && t <= 16 && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
+    if (!c->exact && t <= 64 && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
         return;
     for (int i = 0; i < n; i++)
         product(c, w[i], nullptr, rows[i], cols, xn, cols, t, y[i]);

@@ -394,14 +394,16 @@ def test_round_one_launch_equals_singles(rt, oracle, t, shapes):
 
 
 @pytest.mark.parametrize("shapes", [[8192, 4096, 32, 32], [8192, 1024, 1024], [12288, 12288]], ids=["deltanet_quartet", "attention_qkv", "ffn_pair"])
-@pytest.mark.parametrize("t", [5, 16])
+@pytest.mark.parametrize("t", [5, 16, 17, 40, 64])
 def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
-    """At 5 to 16 tokens a round of products sharing x (rt_gemv_round_dev) runs as one x-resident
-    launch for the products of each wave count and one launch of the partial sums, each product on
-    its own plan: every product's bits are those of its own rt_gemm_dev, at the parity bar, and the
-    round's first kernel is the round kernel (the runtime's kernel records). The 9B DeltaNet quartet
+    """At 5 to 64 tokens a round of products sharing x (rt_gemv_round_dev) runs as one matrix-core
+    launch for the products of each kernel configuration (the x-resident kernel up to 16 tokens,
+    the streaming one above) and one launch of the partial sums, each product on its own plan:
+    every product's bits are those of its own rt_gemm_dev, at the parity bar, and the round's first
+    kernel is a round kernel (the runtime's kernel records). The 9B DeltaNet quartet
     (qwen35.apl:93-96; its 32-row products plan fewer waves than the others), the attention layer's
-    Q, K, V (qwen35.apl:117-119) and a gate and up pair (12288 x 4096)."""
+    Q, K, V (qwen35.apl:117-119) and a gate and up pair (12288 x 4096); at 64 tokens the quartet's
+    partials outgrow the single product's workspace, so the round's own grows."""
     cols = 4096
     n = len(shapes)
     rng = np.random.default_rng(700 + t + n)
@@ -419,7 +421,7 @@ def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
             (kname, _), = _kernels_launched(rt, lambda: rt.lib.rt_gemv_round_dev(rt.R, n, W, R, cols, c.c_void_p(dx), cols, t, Y))
             got = [d.get(p, (t, r), np.float32) for p, r in zip(ys, shapes)]
         say("round", shapes, t, kname)
-        assert kname.startswith("gemm_xres_round<")
+        assert kname.startswith("gemm_xres_round<" if t <= 16 else "gemm_mfma_round<")
         for g, s1, m, r in zip(got, singles, mats, shapes):
             assert np.array_equal(g.view(np.uint32), s1.view(np.uint32)), r
             assert_parity(g, oracle.gemm_f64(m, r, cols, x), f"round {r}x{cols} t={t}")
