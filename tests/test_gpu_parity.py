@@ -516,9 +516,9 @@ def restore_host_mode(rt, old):
 
 @pytest.mark.parametrize("mode", list(HOST_MODES))
 def test_host_pointer_entry_points(rt, mode):
-    """rt_gemv, rt_gemm and a queued round of 4 products sharing x (open/go) give the same bits as the
-    device entry points, with x copied to HBM first or read by the decode kernels from the pinned
-    staging."""
+    """rt_gemv, rt_gemm, a queued round of 4 products sharing x (open/go), a mixed round and queued
+    prompt rounds (6 and 40 tokens) give the same bits as the device entry points, with x copied to
+    HBM first or read by the decode kernels from the pinned staging."""
     rows, cols = 2048, 2048
     rng = np.random.default_rng(31)
     mats = [synth.q8_rows(rng, rows, cols) for _ in range(4)]
@@ -550,6 +550,16 @@ def test_host_pointer_entry_points(rt, mode):
         assert np.array_equal(ys[0].view(np.uint32), want1[2].view(np.uint32))
         assert np.array_equal(ys[1].view(np.uint32), want1[0].view(np.uint32))
         assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, mats[3], rows, cols, x, w=ws[3]).view(np.uint32))
+        # prompt rounds: three queued products sharing x at 6 tokens (the x-resident round) and at
+        # 40 (the streaming one), each the bits of its own device product
+        for t in (6, 40):
+            xt = synth.x_f32(rng, t, cols)
+            Ys = [np.empty((t, rows), np.float32) for _ in range(3)]
+            for w, Yy in zip(ws[:3], Ys):
+                rt.gemm_q(w, rows, cols, xt, t, Yy)
+            rt.gemv_go()
+            for Yy, m, w in zip(Ys, mats, ws):
+                assert np.array_equal(Yy.view(np.uint32), gpu_gemm(rt, m, rows, cols, xt, w=w).view(np.uint32)), t
     finally:
         restore_host_mode(rt, old_mode)
         for w in ws:
