@@ -428,8 +428,9 @@ def prompt_rounds(b):
     alone (its matrix-core kernel and its partial sum) against one round a layer
     (rt_gemv_round_dev: one launch for the products of each kernel configuration, one launch of the
     sums). The 9B DeltaNet quartet (qwen35.apl:93-96), the attention layer's Q, K and V
-    (qwen35.apl:117-119) and the FFN's gate and up (12288 x 4096 each). GB/s counts the weights'
-    bytes."""
+    (qwen35.apl:117-119) and the FFN's gate and up (12288 x 4096 each), the last also as the fused
+    pair SiLU(X Wg^T) * (X Wu^T) (rt_gemv_swiglu_dev: the round with the SwiGLU in its sums' launch).
+    GB/s counts the weights' bytes."""
     out = {}
     for m, name, shapes in [(m, name, shapes) for m in (16, 64) for name, shapes in
                             (("deltanet_quartet", [8192, 4096, 32, 32]), ("attention_qkv", [8192, 1024, 1024]), ("ffn_gate_up", [FFN, FFN]))]:
@@ -449,8 +450,13 @@ def prompt_rounds(b):
             for W in Ws:
                 b.lib.rt_gemv_round_dev(b.R, n, W, R, HIDDEN, c.c_void_p(x), HIDDEN, m, Y)
 
+        def swiglu():  # the FFN's SiLU(X Wg^T) * (X Wu^T) as one call (the round, its sums and the SwiGLU fused)
+            for L in layers:
+                b.pair(L[0], L[1], FFN, HIDDEN, x, m, ys[0])
+
         res = {"weight_bytes": per}
-        for key, fn in (("products_alone", singles), ("one_round", rounds)):
+        runs = (("products_alone", singles), ("one_round", rounds)) + ((("fused_pair_swiglu", swiglu),) if name == "ffn_gate_up" else ())
+        for key, fn in runs:
             fn()  # eager first: the workspace is allocated before the graph records
             b.rt.sync()
             b.lib.rt_graph_begin(b.R)

@@ -259,7 +259,9 @@ long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o);
  * each kernel configuration (at t <= 16 the x-resident kernel's wave count, above it the streaming
  * kernel's) and one launch of every product's partial sums, each product on its own plan (its
  * single launch's bits): 0, or -1 (nothing launched: the partials need more than part_cap floats
- * of part, q8_gemm_round_part_floats; the caller runs them one by one). */
+ * of part, q8_gemm_round_part_floats; the caller runs them one by one). pair_y != NULL: the fused
+ * pair, n == 2 (gate, up; one shape): pair_y = SiLU(G) * U from the two products' sums in one
+ * launch, y[] then only receiving what a product of one split writes itself. */
 struct q8_gemm_round {
     int n;
     const void *w[Q8_ROUND_MAX];
@@ -271,7 +273,7 @@ struct q8_gemm_round {
     long ostart[Q8_ROUND_MAX + 1]; /* first output (t x rows a product); ostart[n] = the outputs */
 };
 int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
-                         float *const *y, float *part, long part_cap, q8_gemm_opts o);
+                         float *const *y, float *part, long part_cap, q8_gemm_opts o, float *pair_y = nullptr);
 long q8_gemm_round_part_floats(int n, const long *rows, long cols, long t, q8_gemm_opts o);
 /* The floor of the x-resident product at 5 <= t <= 16 tokens: its loads on its grid (the plan for
  * these options), no arithmetic, a checksum added to sink[0]; -1 when the plan is not the

@@ -640,6 +640,20 @@ __global__ __launch_bounds__(256) void gemm_sum_round(q8_gemm_round r, long tp)
     r.y[p][j] = split_sum(r.out[p], r.ks[p], tp * r.rows[p], j);
 }
 
+/* The fused pair's end: y[i] = SiLU(G[i]) * U[i], with G and U the gate's and the up product's sums
+ * (products 0 and 1 of the round, the same shape): their split sums in split order, or the Y a
+ * product of one split wrote itself; the same sums and SwiGLU as the two products and the
+ * elementwise kernel apart */
+__global__ __launch_bounds__(256) void gemm_swiglu_round(q8_gemm_round r, long tp, float *y)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= r.ostart[1])
+        return;
+    const float g = r.ks[0] > 1 ? split_sum(r.out[0], r.ks[0], tp * r.rows[0], i) : r.y[0][i];
+    const float u = r.ks[1] > 1 ? split_sum(r.out[1], r.ks[1], tp * r.rows[1], i) : r.y[1][i];
+    y[i] = q8_swiglu(g, u);
+}
+
 /* ---------------------------------------------------------------- launchers */
 
 /* The instantiated configurations of gemm_mfma: MG token tiles a workgroup (the product's MT token
@@ -801,9 +815,9 @@ long q8_gemm_round_part_floats(int n, const long *rows, long cols, long t, q8_ge
 }
 
 int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
-                         float *const *y, float *part, long part_cap, q8_gemm_opts o)
+                         float *const *y, float *part, long part_cap, q8_gemm_opts o, float *pair_y)
 {
-    if (t < 5 || t > 64 || n < 2 || n > Q8_ROUND_MAX)
+    if (t < 5 || t > 64 || n < 2 || n > Q8_ROUND_MAX || (pair_y && (n != 2 || rows[0] != rows[1])))
         return -1;
     q8_gemm_round all;
     gemm_plan pl[Q8_ROUND_MAX];
@@ -863,7 +877,9 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
             abort();
         }
     }
-    if (parts > 0)
+    if (pair_y)
+        gemm_swiglu_round<<<dim3((unsigned)((all.ostart[1] + 255) / 256)), dim3(256), 0, s>>>(all, (t + 15) / 16 * 16, pair_y);
+    else if (parts > 0)
         gemm_sum_round<<<dim3((unsigned)((all.ostart[n] + 255) / 256)), dim3(256), 0, s>>>(all, (t + 15) / 16 * 16);
     return 0;
 }

@@ -280,6 +280,19 @@ float *reserve_epi(ctx *c, size_t n)
     return c->epi;
 }
 
+/* the matrix-core rounds' workspace, at least need floats (grown outside graph capture) */
+float *reserve_rpart(ctx *c, size_t need)
+{
+    if (need > c->rpart_cap) {
+        no_capture(c, "a matrix-core round's partial sums");
+        if (c->rpart)
+            c->retired.push_back(c->rpart);
+        HIPCHECK(hipMalloc((void **)&c->rpart, need * sizeof(float)));
+        c->rpart_cap = need;
+    }
+    return c->rpart;
+}
+
 void reserve_gemm(ctx *c, long rows, long cols, long t)
 {
     if (!c->part && q8_gemm_part_floats(rows, cols, t, c->gemm_opts) > 0) {
@@ -355,6 +368,18 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
         gemm_tokens(c, w0, rows, cols, x, xs, t, y, nullptr, part);
     } else {
         float *g = reserve_scratch(c, (size_t)(2 * rows * t));
+        /* up to 64 tokens the gate and the up product as one round, their sums and the SwiGLU in one
+         * launch (the same sums and SwiGLU as apart); more tokens, 64 at a time apart */
+        const void *w2[2] = {w0, w1};
+        const long r2[2] = {rows, rows};
+        float *y2[2] = {g, g + rows * t};
+        if (t <= 64) {
+            float *rp = reserve_rpart(c, (size_t)q8_gemm_round_part_floats(2, r2, cols, t, c->gemm_opts));
+            if (q8_launch_gemm_round(s, 2, w2, r2, cols, x, xs, t, y2, rp, (long)c->rpart_cap, c->gemm_opts, y) == 0) {
+                launched("the fused pair");
+                return;
+            }
+        }
         gemm_tokens(c, w0, rows, cols, x, xs, t, g);
         gemm_tokens(c, w1, rows, cols, x, xs, t, g + rows * t);
         q8_launch_swiglu_ew(s, g, g + rows * t, rows * t, y);
@@ -435,15 +460,8 @@ bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long co
     if (t <= 4) {
         rc = q8_launch_gemv_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y);
     } else {
-        const size_t need = (size_t)q8_gemm_round_part_floats(n, rows, cols, t, c->gemm_opts);
-        if (need > c->rpart_cap) {
-            no_capture(c, "a matrix-core round's partial sums");
-            if (c->rpart)
-                c->retired.push_back(c->rpart);
-            HIPCHECK(hipMalloc((void **)&c->rpart, need * sizeof(float)));
-            c->rpart_cap = need;
-        }
-        rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y, c->rpart, (long)c->rpart_cap, c->gemm_opts);
+        float *rp = reserve_rpart(c, (size_t)q8_gemm_round_part_floats(n, rows, cols, t, c->gemm_opts));
+        rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y, rp, (long)c->rpart_cap, c->gemm_opts);
     }
     if (rc != 0) {
         if (timed) {

@@ -307,15 +307,24 @@ def test_x_resident_gemm_strided_x_and_residual(rt, ks):
     assert np.array_equal(resid.view(np.uint32), (r + plain).view(np.uint32))
 
 
-def test_fused_pair_many_tokens(rt, oracle):
-    """rt_gemv_swiglu_dev at t >= 5 (two matrix-core products and the SiLU(g)*u epilogue)."""
-    rows, cols, t = 2048, 2048, 8
-    rng = np.random.default_rng(77)
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (2048, 2048), (16, 128)])
+def test_fused_pair_many_tokens(rt, oracle, rows, cols):
+    """rt_gemv_swiglu_dev at t >= 5: up to 64 tokens the gate and up products as one round, with
+    their sums and SiLU(g)*u in one launch; past 64 the products apart, 64 tokens at a time, and the
+    elementwise SwiGLU. A token's bits do not depend on t, so the first tokens at t = 70 (apart)
+    equal t = 5, 16 and 64 (the round) bit for bit, and every result meets the parity bar against
+    F64 (the first 8 tokens on 12288 x 4096). 16 x 128 has one K split: its products write their
+    sums themselves."""
+    rng = np.random.default_rng(77 + rows)
     q8g, q8u = synth.q8_rows(rng, rows, cols), synth.q8_rows(rng, rows, cols)
-    x = synth.x_f32(rng, t, cols)
-    got = gpu_swiglu(rt, q8g, q8u, rows, cols, x)
-    want = oracle.swiglu_f64(oracle.gemm_f64(q8g, rows, cols, x), oracle.gemm_f64(q8u, rows, cols, x))
-    assert_parity(got, want, "swiglu t=8")
+    x = synth.x_f32(rng, 70, cols)
+    y70 = gpu_swiglu(rt, q8g, q8u, rows, cols, x)
+    for t in (5, 16, 64):
+        yt = gpu_swiglu(rt, q8g, q8u, rows, cols, x[:t])
+        assert np.array_equal(yt.view(np.uint32), y70[:t].view(np.uint32)), t
+    tc = 8 if rows * cols > 1 << 24 else 70
+    want = oracle.swiglu_f64(oracle.gemm_f64(q8g, rows, cols, x[:tc]), oracle.gemm_f64(q8u, rows, cols, x[:tc]))
+    assert_parity(y70[:tc], want, f"swiglu {rows}x{cols}")
 
 
 def test_graph_replays_match_eager(rt):
