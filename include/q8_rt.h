@@ -157,8 +157,8 @@ void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, cons
 void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t, float *const *y);
 /* The FFN's fused pair: Y[k] = SiLU(G[k]) * U[k] with G = X Wg^T and U = X Wu^T, both [rows cols],
  * x read once for both; SiLU(g) = g / (1 + exp(-g)) (src/apl/qwen35.apl:38, 125). t tokens: up to
- * 4 one decode launch; 5 to 64 the two products as a matrix-core round and their sums with the
- * SwiGLU in one more launch; more, the products apart, 64 tokens at a time, then the SwiGLU. */
+ * 4 one decode launch; from 5, 64 tokens at a time, the two products as a matrix-core round and
+ * their sums with the SwiGLU in one more launch. */
 void rt_gemv_swiglu_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* ---- the epilogues on either side of a product (additions; the reference computes them on its
  * host around the products: RMS = {⍺×⍵×(RMS_EPS+(+/⍵×⍵)÷≢⍵)*¯0.5}, src/apl/qwen35.apl:49, before a

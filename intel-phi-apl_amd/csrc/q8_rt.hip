@@ -368,17 +368,25 @@ void product(ctx *c, const void *w0, const void *w1, long rows, long cols, const
         gemm_tokens(c, w0, rows, cols, x, xs, t, y, nullptr, part);
     } else {
         float *g = reserve_scratch(c, (size_t)(2 * rows * t));
-        /* up to 64 tokens the gate and the up product as one round, their sums and the SwiGLU in one
-         * launch (the same sums and SwiGLU as apart); more tokens, 64 at a time apart */
+        /* 64 tokens at a time, the gate and the up product as one round, their sums and the SwiGLU
+         * in one launch: the same sums and SwiGLU as apart (below, where the round is refused) */
         const void *w2[2] = {w0, w1};
         const long r2[2] = {rows, rows};
-        float *y2[2] = {g, g + rows * t};
-        if (t <= 64) {
-            float *rp = reserve_rpart(c, (size_t)q8_gemm_round_part_floats(2, r2, cols, t, c->gemm_opts));
-            if (q8_launch_gemm_round(s, 2, w2, r2, cols, x, xs, t, y2, rp, (long)c->rpart_cap, c->gemm_opts, y) == 0) {
-                launched("the fused pair");
-                return;
+        const long t0 = t < 64 ? t : 64;
+        float *rp = reserve_rpart(c, (size_t)q8_gemm_round_part_floats(2, r2, cols, t0, c->gemm_opts));
+        bool pair_done = true;
+        for (long k = 0; k < t && pair_done; k += 64) {
+            const long tk = t - k < 64 ? t - k : 64;
+            float *y2[2] = {g, g + rows * tk};
+            if (q8_launch_gemm_round(s, 2, w2, r2, cols, x + k * xs, xs, tk, y2, rp, (long)c->rpart_cap, c->gemm_opts, y + k * rows) != 0) {
+                if (k > 0)
+                    fail("the fused pair", "a later 64-token chunk refused its round (a planning error)");
+                pair_done = false;
             }
+        }
+        if (pair_done) {
+            launched("the fused pair");
+            return;
         }
         gemm_tokens(c, w0, rows, cols, x, xs, t, g);
         gemm_tokens(c, w1, rows, cols, x, xs, t, g + rows * t);

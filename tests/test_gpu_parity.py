@@ -309,12 +309,11 @@ def test_x_resident_gemm_strided_x_and_residual(rt, ks):
 
 @pytest.mark.parametrize("rows,cols", [(12288, 4096), (2048, 2048), (16, 128)])
 def test_fused_pair_many_tokens(rt, oracle, rows, cols):
-    """rt_gemv_swiglu_dev at t >= 5: up to 64 tokens the gate and up products as one round, with
-    their sums and SiLU(g)*u in one launch; past 64 the products apart, 64 tokens at a time, and the
-    elementwise SwiGLU. A token's bits do not depend on t, so the first tokens at t = 70 (apart)
-    equal t = 5, 16 and 64 (the round) bit for bit, and every result meets the parity bar against
-    F64 (the first 8 tokens on 12288 x 4096). 16 x 128 has one K split: its products write their
-    sums themselves."""
+    """rt_gemv_swiglu_dev at t >= 5: 64 tokens at a time, the gate and up products as one round,
+    with their sums and SiLU(g)*u in one launch. A token's bits do not depend on t, so the first
+    tokens at t = 70 (a 64-token round and a 6-token one) equal t = 5, 16 and 64 bit for bit, and
+    every result meets the parity bar against F64 (the first 8 tokens on 12288 x 4096). 16 x 128
+    has one K split: its products write their sums themselves."""
     rng = np.random.default_rng(77 + rows)
     q8g, q8u = synth.q8_rows(rng, rows, cols), synth.q8_rows(rng, rows, cols)
     x = synth.x_f32(rng, 70, cols)
