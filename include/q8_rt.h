@@ -84,8 +84,8 @@ void rt_fini(struct rt *R);
 void rt_gemv(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
 
 /* Adjacent products: queue up to RT_BATCH, none reading another's result; rt_gemv_go runs them
- * all and returns when every y is valid. Queued products that share x copy it once and, at up to
- * 64 tokens, run as a round (rt_gemv_round_dev, below).
+ * all and returns when every y is valid. Queued products that share x copy it once and run as a
+ * round (rt_gemv_round_dev, below).
  * (rt.h:63-69; rt.c:251-265, 274-285) */
 #define RT_BATCH 8
 void rt_gemv_q(struct rt *R, const void *w, long rows, long cols, const float *x, float *y);
@@ -148,9 +148,9 @@ void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float 
  * two runtimes) race. */
 void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* A round of n (1..RT_BATCH) products sharing x, none reading another's y: y[i] = X w[i]^T,
- * w[i] [rows[i] cols]. At t <= 4 one launch where the decode kernel takes the shapes; at 5 <= t
- * <= 64 one matrix-core launch for the products of each kernel configuration and one launch of
- * their partial sums (each product on its own plan); otherwise one product after another. Each y has
+ * w[i] [rows[i] cols]. At t <= 4 one launch where the decode kernel takes the shapes; from 5
+ * tokens, 64 at a time, one matrix-core launch for the products of each kernel configuration and
+ * one launch of their partial sums (each product on its own plan). Each y has
  * the bits of its own single product. The device form of rt_gemv_q x n + rt_gemv_go, which uses
  * the same launches for queued products that share x (the DeltaNet quartet QKV/GATE/BETA/ALPHA,
  * src/apl/qwen35.apl:93-96; the attention layer's Q/K/V, qwen35.apl:117-119). */
@@ -178,7 +178,7 @@ void rt_gemm_norm_dev(struct rt *R, const void *w, long rows, long cols, const f
 void rt_gemv_swiglu_norm_dev(struct rt *R, const void *wg, const void *wu, long rows, long cols, const float *x, long x_stride, long t, const float *nw,
                              float eps, float *y);
 /* A round of products sharing RMS(X) (the DeltaNet quartet on W_ANORM RMS X): at t <= 4 one
- * launch with the norm fused; at 5 <= t <= 64 the norm, then the round's launches as above. */
+ * launch with the norm fused; from 5 tokens the norm, then the round's launches as above. */
 void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
                             const float *nw, float eps, float *const *y);
 /* Y = R + X W^T (after W_OUT and W_DOWN); r [t rows] may be y, the residual stream updated in place. */

@@ -448,9 +448,9 @@ void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, c
     launched("the residual add");
 }
 
-/* Products sharing x as one launch: at t <= 4 the decode round, at 5 <= t <= 64 the matrix-core
- * round (one launch a kernel configuration, each product on its own plan, so with its own
- * launch's bits) and one launch of their partial sums, in a workspace of its own grown to the
+/* Products sharing x as one launch: at t <= 4 the decode round, from 5 tokens, 64 at a time, the
+ * matrix-core round (one launch a kernel configuration, each product on its own plan, so with its
+ * own launch's bits) and one launch of their partial sums, in a workspace of its own grown to the
  * round. True when launched, false when the kernels do not take the shapes (the caller then runs
  * them one by one). */
 bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long cols, const float *x, long xs, long t, float *const *y)
@@ -468,8 +468,18 @@ bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long co
     if (t <= 4) {
         rc = q8_launch_gemv_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y);
     } else {
-        float *rp = reserve_rpart(c, (size_t)q8_gemm_round_part_floats(n, rows, cols, t, c->gemm_opts));
-        rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x, xs, t, y, rp, (long)c->rpart_cap, c->gemm_opts);
+        /* 64 tokens at a time (a token's bits do not depend on t) */
+        float *rp = reserve_rpart(c, (size_t)q8_gemm_round_part_floats(n, rows, cols, t < 64 ? t : 64, c->gemm_opts));
+        rc = 0;
+        for (long k = 0; k < t && rc == 0; k += 64) {
+            const long tk = t - k < 64 ? t - k : 64;
+            float *yk[RT_BATCH];
+            for (int i = 0; i < n; i++)
+                yk[i] = y[i] + k * rows[i];
+            rc = q8_launch_gemm_round((q8_stream_t)c->stream, n, w, rows, cols, x + k * xs, xs, tk, yk, rp, (long)c->rpart_cap, c->gemm_opts);
+            if (rc != 0 && k > 0)
+                fail("the round", "a later 64-token chunk refused its round (a planning error)");
+        }
     }
     if (rc != 0) {
         if (timed) {
@@ -569,10 +579,10 @@ void run_round(ctx *c, job *jobs, int n, const char *what)
         q8_launch_copy((q8_stream_t)c->stream, c->dx, c->hx, (long)(nx / 4)); /* nx is a multiple of 64 floats */
         launched("the copy of x");
     }
-    /* products that share x (and t <= 64): one round for the group */
+    /* products that share x (and t): one round for the group */
     bool done[RT_BATCH] = {};
     for (int i = 0; i < n && !c->exact; i++) {
-        if (done[i] || jobs[i].t > 64)
+        if (done[i])
             continue;
         const void *w[RT_BATCH];
         long rows[RT_BATCH];
@@ -953,7 +963,7 @@ void rt_gemv_round_dev(struct rt *R, int n, const void *const *w, const long *ro
         check_shape(c, "rt_gemv_round_dev", w[i], rows[i], cols);
         check_dev_ptr("rt_gemv_round_dev", y[i], "every y");
     }
-    if (!c->exact && t <= 64 && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
+    if (!c->exact && n > 1 && round_launch(c, n, w, rows, cols, x, x_stride, t, y))
         return;
     for (int i = 0; i < n; i++)
         product(c, w[i], nullptr, rows[i], cols, x, x_stride, t, y[i]);
@@ -1043,7 +1053,7 @@ void rt_gemv_round_norm_dev(struct rt *R, int n, const void *const *w, const lon
     float *xn = reserve_epi(c, (size_t)(t * cols));
     q8_launch_rmsnorm(s, x, x_stride, t, cols, nw, eps, xn);
     launched("the norm");
-    if (!c->exact && t <= 64 && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
+    if (!c->exact && n > 1 && round_launch(c, n, w, rows, cols, xn, cols, t, y))
         return;
     for (int i = 0; i < n; i++)
         product(c, w[i], nullptr, rows[i], cols, xn, cols, t, y[i]);
