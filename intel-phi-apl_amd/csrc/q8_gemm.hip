@@ -717,15 +717,22 @@ static long resident_xres(int nw)
  * hold fewer), a function of the shape alone (nw comes from the shape too), so that a token's
  * output has the same bits whatever the number of tokens it is computed with (5 to 64 a launch,
  * and every 64-token launch of a longer X). As many splits as fill the device with one resident
- * round of the x-resident kernel's workgroups (16 nw rows each), fewer if the partials of a
- * 64-token launch would not fit the workspace. ks_force > 0 sets the split count instead (a test
- * hook: other splits, other bits). */
+ * round of the x-resident kernel's workgroups (16 nw rows each), with at least two ranges a split
+ * above 256 rows, fewer if the partials of a 64-token launch would not fit the workspace. Above
+ * 256 rows one-range splits write and add more partials than their shorter streams save: 1024 x
+ * 4096 at 16 splits of two ranges took 10.1 us at 16 tokens and 14.4 at 64, against 10.7 and 15.3
+ * at 32 splits of one. At 256 rows or fewer the grid is a few workgroups on an otherwise idle
+ * device, the product takes one workgroup's time, and a second range lengthens it (the two
+ * 32 x 4096 products of a 64-token round took ~2 us more at two ranges a split). ks_force > 0 sets
+ * the split count instead (a test hook: other splits, other bits). */
 static void split_of(long rows, long cols, int nw, int ks_force, int *ks, int *cps)
 {
     const long tiles = (rows + 16L * nw - 1) / (16L * nw);
     const long np = ((cols / Q8_BLOCK) + 1) / 2;
     const long ranges = (np + XRES_KP - 1) / XRES_KP;
     long split = ks_force > 0 ? ks_force : resident_xres(nw) / tiles;
+    if (ks_force <= 0 && rows > 256 && split > ranges / 2)
+        split = ranges / 2;
     split = split < 1 ? 1 : split > ranges ? ranges : split;
     long per = (ranges + split - 1) / split;
     while (per < ranges && (ranges + per - 1) / per * 64 * rows > Q8_GEMM_PART_MAX)
