@@ -812,7 +812,7 @@ static void round_plan(int n, const void *const *w, const long *rows, long cols,
 
 long q8_gemm_round_part_floats(int n, const long *rows, long cols, long t, q8_gemm_opts o)
 {
-    if (t < 5 || t > 64 || n < 2 || n > Q8_ROUND_MAX)
+    if (t < 1 || t > 64 || n < 2 || n > Q8_ROUND_MAX)
         return 0;
     q8_gemm_round all;
     gemm_plan pl[Q8_ROUND_MAX];
@@ -824,7 +824,7 @@ long q8_gemm_round_part_floats(int n, const long *rows, long cols, long t, q8_ge
 int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const long *rows, long cols, const float *x, long x_stride, long t,
                          float *const *y, float *part, long part_cap, q8_gemm_opts o, float *pair_y)
 {
-    if (t < 5 || t > 64 || n < 2 || n > Q8_ROUND_MAX || (pair_y && (n != 2 || rows[0] != rows[1])))
+    if (t < 1 || t > 64 || n < 2 || n > Q8_ROUND_MAX || (pair_y && (n != 2 || rows[0] != rows[1])))
         return -1;
     q8_gemm_round all;
     gemm_plan pl[Q8_ROUND_MAX];

@@ -311,14 +311,15 @@ def test_x_resident_gemm_strided_x_and_residual(rt, ks):
 def test_fused_pair_many_tokens(rt, oracle, rows, cols):
     """rt_gemv_swiglu_dev at t >= 5: 64 tokens at a time, the gate and up products as one round,
     with their sums and SiLU(g)*u in one launch. A token's bits do not depend on t, so the first
-    tokens at t = 70 (a 64-token round and a 6-token one) equal t = 5, 16 and 64 bit for bit, and
-    every result meets the parity bar against F64 (the first 8 tokens on 12288 x 4096). 16 x 128
-    has one K split: its products write their sums themselves."""
+    tokens at t = 70 (a 64-token round and a 6-token one) equal t = 5, 16, 64, 65 and 68 bit for bit
+    (the last two end with a round of 1 and 4 tokens), and every result meets the parity bar against
+    F64 (the first 8 tokens on 12288 x 4096). 16 x 128 has one K split: its products write their
+    sums themselves."""
     rng = np.random.default_rng(77 + rows)
     q8g, q8u = synth.q8_rows(rng, rows, cols), synth.q8_rows(rng, rows, cols)
     x = synth.x_f32(rng, 70, cols)
     y70 = gpu_swiglu(rt, q8g, q8u, rows, cols, x)
-    for t in (5, 16, 64):
+    for t in (5, 16, 64, 65, 68):
         yt = gpu_swiglu(rt, q8g, q8u, rows, cols, x[:t])
         assert np.array_equal(yt.view(np.uint32), y70[:t].view(np.uint32)), t
     tc = 8 if rows * cols > 1 << 24 else 70
@@ -402,7 +403,7 @@ def test_round_one_launch_equals_singles(rt, oracle, t, shapes):
 
 
 @pytest.mark.parametrize("shapes", [[8192, 4096, 32, 32], [8192, 1024, 1024], [12288, 12288]], ids=["deltanet_quartet", "attention_qkv", "ffn_pair"])
-@pytest.mark.parametrize("t", [5, 16, 17, 40, 64, 70])
+@pytest.mark.parametrize("t", [5, 16, 17, 40, 64, 65, 68, 70])
 def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
     """From 5 tokens, 64 at a time, a round of products sharing x (rt_gemv_round_dev) runs as one
     matrix-core launch for the products of each kernel configuration (the x-resident kernel up to
@@ -412,7 +413,9 @@ def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
     kernel is a round kernel (the runtime's kernel records). The 9B DeltaNet quartet
     (qwen35.apl:93-96; its 32-row products plan fewer waves than the others), the attention layer's
     Q, K, V (qwen35.apl:117-119) and a gate and up pair (12288 x 4096); at 64 tokens the quartet's
-    partials outgrow the single product's workspace, so the round's own grows."""
+    partials outgrow the single product's workspace, so the round's own grows. At 65 and 68 tokens
+    the last chunk holds 1 and 4 tokens: it runs as a matrix-core round too, as the single
+    product's last chunk runs on the matrix cores."""
     cols = 4096
     n = len(shapes)
     rng = np.random.default_rng(700 + t + n)
@@ -559,9 +562,10 @@ def test_host_pointer_entry_points(rt, mode):
         assert np.array_equal(ys[0].view(np.uint32), want1[2].view(np.uint32))
         assert np.array_equal(ys[1].view(np.uint32), want1[0].view(np.uint32))
         assert np.array_equal(Y.view(np.uint32), gpu_gemm(rt, mats[3], rows, cols, x, w=ws[3]).view(np.uint32))
-        # prompt rounds: three queued products sharing x at 6 tokens (the x-resident round) and at
-        # 40 (the streaming one), each the bits of its own device product
-        for t in (6, 40):
+        # prompt rounds: three queued products sharing x at 6 tokens (the x-resident round), at 40
+        # (the streaming one) and at 66 (a 64-token round, then one of 2 tokens), each the bits of
+        # its own device product
+        for t in (6, 40, 66):
             xt = synth.x_f32(rng, t, cols)
             Ys = [np.empty((t, rows), np.float32) for _ in range(3)]
             for w, Yy in zip(ws[:3], Ys):
