@@ -745,7 +745,10 @@ static void split_of(long rows, long cols, int nw, int ks_force, int *ks, int *c
  * stay independent of t): the one whose grid takes the fewest rounds of resident workgroups times
  * the rows and ranges a workgroup streams; 16 on a tie. At 12288 x 4096, 16 waves make 48 row
  * tiles x 5 splits = 240 workgroups of 256 rows x 7 ranges, 16 compute units idle; 12 make 64 x 4
- * = 256 of 192 rows x 8 ranges. At 4096 x 12288 16 waves fill the device (16 x 16 of 256 x 6). */
+ * = 256 of 192 rows x 8 ranges. At 4096 x 12288 16 waves fill the device (16 x 16 of 256 x 6). A
+ * matrix of at most 192 rows is one row tile either way, with the same split and the same rows a
+ * workgroup, so it ties and takes 16 waves, as a round's larger products do: the DeltaNet
+ * quartet's 32-row products then share their launch. */
 static int nw_of(long rows, long cols, int ks_force)
 {
     long best = -1;
@@ -754,7 +757,7 @@ static int nw_of(long rows, long cols, int ks_force)
         int ks, cps;
         split_of(rows, cols, nw, ks_force, &ks, &cps);
         const long tiles = (rows + 16L * nw - 1) / (16L * nw), res = resident_xres(nw);
-        const long cost = (tiles * ks + res - 1) / res * 16L * nw * cps;
+        const long cost = (tiles * ks + res - 1) / res * (rows < 16L * nw ? rows : 16L * nw) * cps;
         if (best < 0 || cost < best) {
             best = cost;
             pick = nw;

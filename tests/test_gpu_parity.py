@@ -411,7 +411,7 @@ def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
     plan:
     every product's bits are those of its own rt_gemm_dev, at the parity bar, and the round's first
     kernel is a round kernel (the runtime's kernel records). The 9B DeltaNet quartet
-    (qwen35.apl:93-96; its 32-row products plan fewer waves than the others), the attention layer's
+    (qwen35.apl:93-96; its 32-row products are one row tile with 14 idle waves), the attention layer's
     Q, K, V (qwen35.apl:117-119) and a gate and up pair (12288 x 4096); at 64 tokens the quartet's
     partials outgrow the single product's workspace, so the round's own grows. At 65 and 68 tokens
     the last chunk holds 1 and 4 tokens: it runs as a matrix-core round too, as the single
