@@ -426,8 +426,7 @@ def prompt_rounds(b):
     """At M = 16 and 64 tokens (a prompt chunk, a speculative verify), three rounds of products that
     share x, over 32 layers of distinct weights, each recorded as a graph: every product launched
     alone (its matrix-core kernel and its partial sum) against one round a layer
-    (rt_gemv_round_dev: one launch for the products of each kernel configuration, one launch of the
-    sums). The 9B DeltaNet quartet (qwen35.apl:93-96), the attention layer's Q, K and V
+    (rt_gemv_round_dev: one launch for the products, one launch of the sums). The 9B DeltaNet quartet (qwen35.apl:93-96), the attention layer's Q, K and V
     (qwen35.apl:117-119) and the FFN's gate and up (12288 x 4096 each), the last also as the fused
     pair SiLU(X Wg^T) * (X Wu^T) (rt_gemv_swiglu_dev: the round with the SwiGLU in its sums' launch).
     GB/s counts the weights' bytes."""

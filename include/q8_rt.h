@@ -149,8 +149,8 @@ void rt_gemm_dev(struct rt *R, const void *w, long rows, long cols, const float 
 void rt_gemm_dev_noalloc(struct rt *R, const void *w, long rows, long cols, const float *x, long x_stride, long t, float *y);
 /* A round of n (1..RT_BATCH) products sharing x, none reading another's y: y[i] = X w[i]^T,
  * w[i] [rows[i] cols]. At t <= 4 one launch where the decode kernel takes the shapes; from 5
- * tokens, 64 at a time, one matrix-core launch for the products of each kernel configuration and
- * one launch of their partial sums (each product on its own plan). Each y has
+ * tokens, 64 at a time, one matrix-core launch for the products and one launch of their partial
+ * sums (each product on its own K split). Each y has
  * the bits of its own single product. The device form of rt_gemv_q x n + rt_gemv_go, which uses
  * the same launches for queued products that share x (the DeltaNet quartet QKV/GATE/BETA/ALPHA,
  * src/apl/qwen35.apl:93-96; the attention layer's Q/K/V, qwen35.apl:117-119). */

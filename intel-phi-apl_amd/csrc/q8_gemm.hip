@@ -278,8 +278,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows
     mfma_body<MT, RT, KP, NW>(w, rows, cols, x, x_stride, t, ks, cps, part, y, res, blockIdx.x);
 }
 
-/* A round of products sharing x (17 <= t <= 64) of one configuration as one launch: workgroup
- * (b, g) runs position (b - start[p], g) of product p's own grid on its own plan */
+/* A round of products sharing x (17 <= t <= 64) as one launch: workgroup (b, g) runs position
+ * (b - start[p], g) of product p's grid at this launch's NW, on the product's own K split */
 template <int MT, int RT, int KP, int NW>
 __global__ __launch_bounds__(64 * NW) void gemm_mfma_round(q8_gemm_round r, long cols, const float *x, long x_stride, long t)
 {
@@ -465,8 +465,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows
 }
 
 /* A round of products that share x (and t <= 16) as one launch: workgroup b belongs to product p
- * with start[p] <= b < start[p+1] and runs that product's own grid position b - start[p] on its
- * own plan, so every product gets the bits of its own launch. */
+ * with start[p] <= b < start[p+1] and runs position b - start[p] of that product's grid at this
+ * launch's NW, on the product's own K split, so every product gets the bits of its own launch. */
 template <int KP, int NW, int SC>
 __global__ __launch_bounds__(64 * NW) void gemm_xres_round(q8_gemm_round r, long cols, const float *x, long x_stride, long t)
 {
@@ -836,19 +836,31 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
     if (parts > part_cap || (parts > 0 && !part))
         return -1;
     hipStream_t s = (hipStream_t)stream;
-    /* one launch for the products of each kernel configuration (the x-resident kernel's wave count,
-     * or the streaming kernel's MG, RT, KP, NW), then every product's sums */
+    /* one launch for the products of each kernel configuration (the x-resident kernel, or the
+     * streaming kernel's MG, RT and KP: with these plans one launch for the whole round), at the
+     * wave count of its largest product, then every product's sums. The waves a workgroup only
+     * decide which rows a workgroup streams; each product keeps its own K split, and so the bits
+     * of its own launch (the attention layer's K and V, 1024 x 4096, plan 12 waves alone and run
+     * at Q's 16 in its round) */
     bool launched[Q8_ROUND_MAX] = {};
     for (int p0 = 0; p0 < n; p0++) {
         if (launched[p0])
             continue;
         const gemm_plan &c0 = pl[p0];
-        const int rowsper = 16 * c0.c.nw * (c0.xres ? 1 : c0.c.rt);
+        auto same = [&](int p) {
+            return !launched[p] && pl[p].xres == c0.xres && (c0.xres || (pl[p].c.mg == c0.c.mg && pl[p].c.rt == c0.c.rt && pl[p].c.kp == c0.c.kp));
+        };
+        int nw = c0.c.nw;
+        for (long p = p0 + 1, big = rows[p0]; p < n; p++)
+            if (same((int)p) && rows[p] > big) {
+                big = rows[p];
+                nw = pl[p].c.nw;
+            }
+        const int rowsper = 16 * nw * (c0.xres ? 1 : c0.c.rt);
         q8_gemm_round g{};
         long wgs = 0;
         for (int p = p0; p < n; p++) {
-            if (launched[p] || pl[p].xres != c0.xres || pl[p].c.nw != c0.c.nw ||
-                (!c0.xres && (pl[p].c.mg != c0.c.mg || pl[p].c.rt != c0.c.rt || pl[p].c.kp != c0.c.kp)))
+            if (!same(p))
                 continue;
             launched[p] = true;
             const int k = g.n++;
@@ -864,7 +876,7 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
         g.start[g.n] = wgs;
         bool ok = false;
         if (c0.xres) {
-            if (c0.c.nw == 12)
+            if (nw == 12)
                 Q8_LAUNCH(q8_time_name("gemm_xres_round", 3, XRES_KP, 12, XRES_SC), (gemm_xres_round<XRES_KP, 12, XRES_SC>), dim3((unsigned)wgs),
                           dim3(64 * 12), s, g, cols, x, x_stride, t);
             else
@@ -874,7 +886,7 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
         } else {
             const unsigned groups = (unsigned)(((t + 15) / 16 + c0.c.mg - 1) / c0.c.mg);
 #define GR(G, R, P, N)                                                                                                 \
-    if (!ok && c0.c.mg == G && c0.c.rt == R && c0.c.kp == P && c0.c.nw == N) {                                         \
+    if (!ok && c0.c.mg == G && c0.c.rt == R && c0.c.kp == P && nw == N) {                                              \
         Q8_LAUNCH(q8_time_name("gemm_mfma_round", 4, G, R, P, N), (gemm_mfma_round<G, R, P, N>), dim3((unsigned)wgs, groups), dim3(64 * N), s, g,    \
                   cols, x, x_stride, t);                                                                               \
         ok = true;                                                                                                     \
@@ -883,7 +895,7 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
 #undef GR
         }
         if (!ok) {
-            fprintf(stderr, "q8_gemm: no round kernel for MG %d RT %d KP %d NW %d\n", c0.c.mg, c0.c.rt, c0.c.kp, c0.c.nw);
+            fprintf(stderr, "q8_gemm: no round kernel for MG %d RT %d KP %d NW %d\n", c0.c.mg, c0.c.rt, c0.c.kp, nw);
             abort();
         }
     }

@@ -449,8 +449,8 @@ void product_epi(ctx *c, const void *w0, const void *w1, long rows, long cols, c
 }
 
 /* Products sharing x as one launch: at t <= 4 the decode round, from 5 tokens, 64 at a time, the
- * matrix-core round (one launch a kernel configuration, each product on its own plan, so with its
- * own launch's bits) and one launch of their partial sums, in a workspace of its own grown to the
+ * matrix-core round (one launch, each product on its own K split, so with its own launch's bits)
+ * and one launch of their partial sums, in a workspace of its own grown to the
  * round. True when launched, false when the kernels do not take the shapes (the caller then runs
  * them one by one). */
 bool round_launch(ctx *c, int n, const void *const *w, const long *rows, long cols, const float *x, long xs, long t, float *const *y)

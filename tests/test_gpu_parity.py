@@ -406,9 +406,9 @@ def test_round_one_launch_equals_singles(rt, oracle, t, shapes):
 @pytest.mark.parametrize("t", [5, 16, 17, 40, 64, 65, 68, 70])
 def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
     """From 5 tokens, 64 at a time, a round of products sharing x (rt_gemv_round_dev) runs as one
-    matrix-core launch for the products of each kernel configuration (the x-resident kernel up to
-    16 tokens, the streaming one above) and one launch of the partial sums, each product on its own
-    plan:
+    matrix-core launch for the products (the x-resident kernel up to 16 tokens, the streaming one
+    above, at the largest product's wave count) and one launch of the partial sums, each product on
+    its own K split:
     every product's bits are those of its own rt_gemm_dev, at the parity bar, and the round's first
     kernel is a round kernel (the runtime's kernel records). The 9B DeltaNet quartet
     (qwen35.apl:93-96; its 32-row products are one row tile with 14 idle waves), the attention layer's
