@@ -301,9 +301,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_round(q8_gemm_round r, long
  * the scales for every range, and waits for them and for a barrier before each range's MFMAs.
  * The sums are gemm_mfma's in the same order, so on the same split the two give the same bits.
  * blk: the workgroup's index in the product's grid (tile blk / ks, split blk % ks). */
-template <int KP, int NW, int SC>
-__device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
-                                          float *part, float *y, const float *res, unsigned blk)
+template <int KP, int NW, int SC, int NP = 1>
+__device__ __forceinline__ void xres_body(const uint8_t *const (&w)[NP], long rows, long cols, const float *x, long x_stride, long t, int ks,
+                                          int cps, float *const (&part)[NP], float *const (&y)[NP], const float *res, unsigned blk)
 {
     constexpr int BS = 2 * KP * SC;                     /* blocks of a segment */
     constexpr int XS = 64 * BS;                         /* x lane slots of a segment: 8 values of one token */
@@ -312,7 +312,8 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
     constexpr int DR = (DN + 64 * NW - 1) / (64 * NW);
     constexpr int DP = BS + 2;                          /* scale row pitch in LDS (halves): an odd dword count, no bank conflicts */
     __shared__ uint4 xls[BS * 3 * 64];                  /* [block][limb][lane] */
-    __shared__ uint16_t dls[NW * 16 * DP];              /* [row of the workgroup][block] */
+    constexpr int DL = NW * 16 * DP;                    /* a product's scales in LDS (halves) */
+    __shared__ uint16_t dls[NP * DL];                   /* [product][row of the workgroup][block] */
     const int lane = threadIdx.x & 63;
     /* the wave's index, uniform: everything derived from it (the row tile, whether the wave is
      * live, the range tests) stays in scalar registers */
@@ -326,18 +327,30 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
     const bool live = rt0 < rows / 16;
     const int n = lane & 15, kq = lane >> 4;
     /* the row tile's weights at a uniform base; the lane's row and 16 bytes at a 32-bit offset */
-    const uint8_t *wt = w + q8s_row_q(live ? rt0 * 16 : 0, cols);
+    const uint8_t *wt[NP];
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++)
+        wt[pp] = w[pp] + q8s_row_q(live ? rt0 * 16 : 0, cols);
     const unsigned woff = (unsigned)(n * cols + 16 * kq);
 
-    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    /* acc: the sums of the product being streamed (product 0 at a segment's start); oth: the other
+     * product's of a pair */
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, oth = acc;
     const int r0 = split * cps, nr = (np + KP - 1) / KP;
     const int mine = nr - r0 < cps ? nr - r0 : cps; /* the last split may hold fewer ranges */
     for (int sb = 0; sb < mine; sb += SC) {
         const int nc = mine - sb < SC ? mine - sb : SC;
         const int c00 = (r0 + sb) * KP, b0 = 2 * c00; /* the segment's first pair and block */
+        /* step e of the segment's stream: the range of product pe it reads (a pair streams product
+         * 0's nc ranges, then product 1's); past the last step, the last range again */
+        auto step = [&](int e, int &pe) {
+            pe = NP == 2 && e >= nc ? 1 : 0;
+            const int rr = e - pe * nc;
+            return rr < nc ? rr : nc - 1;
+        };
         uint4 q[2][KP];
         float4 xr[XR][2];
-        uint16_t dr[DR];
+        uint16_t dr[NP][DR];
         /* every load of the segment's x and scales, then ranges 0 and 1's weights, all unconditional
          * from clamped indices (what lies past t or past the last block is zeroed after the loads):
          * two ranges in flight while the x limbs are made, as during the stream */
@@ -353,23 +366,29 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
             xr[k][1] = *(const float4 *)(px + 4);
         }
 #pragma unroll
-        for (int k = 0; k < DR; k++) {
-            const int s = (int)threadIdx.x + 64 * NW * k;
-            long row = tile * NW * 16 + s / BS;
-            row = row < rows ? row : rows - 1;
-            int b = b0 + s % BS;
-            b = b < nb ? b : nb - 1;
-            dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
-        }
+        for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+            for (int k = 0; k < DR; k++) {
+                const int s = (int)threadIdx.x + 64 * NW * k;
+                long row = tile * NW * 16 + s / BS;
+                row = row < rows ? row : rows - 1;
+                int b = b0 + s % BS;
+                b = b < nb ? b : nb - 1;
+                dr[pp][k] = ((const uint16_t *)(w[pp] + q8s_row_d(row, cols)))[b];
+            }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+        for (int h = 0; h < 2; h++) {
+            int ph;
+            const int rr = step(h, ph);
+            const uint8_t *wh = NP == 2 && ph ? wt[NP - 1] : wt[0];
 #pragma unroll
             for (int p = 0; p < KP; p++) {
-                int c = c00 + (h < nc ? h : nc - 1) * KP + p;
+                int c = c00 + rr * KP + p;
                 c = c < np ? c : np - 1;
-                q[h][p] = *(const uint4 *)(wt + 64L * c + woff);
+                q[h][p] = *(const uint4 *)(wh + 64L * c + woff);
             }
+        }
         __builtin_amdgcn_sched_barrier(0);
         /* the segment's x limbs and scales into LDS (waits for them, not for the weights) */
 #pragma unroll
@@ -387,25 +406,38 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
             }
         }
 #pragma unroll
-        for (int k = 0; k < DR; k++) {
-            const int s = (int)threadIdx.x + 64 * NW * k;
-            if (DN % (64 * NW) == 0 || s < DN)
-                dls[(s / BS) * DP + s % BS] = dr[k];
-        }
+        for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+            for (int k = 0; k < DR; k++) {
+                const int s = (int)threadIdx.x + 64 * NW * k;
+                if (DN % (64 * NW) == 0 || s < DN)
+                    dls[pp * DL + (s / BS) * DP + s % BS] = dr[pp][k];
+            }
         __syncthreads();
         /* the segment's ranges, unrolled whole (a loop back edge would drain the loads in flight):
          * range ch's MFMAs (range ch+1 in flight), then range ch+2 issued into its registers (past
-         * the last, range nc-1 again, from L2) */
+         * the last, range nc-1 again, from L2). A pair's 2 SC steps skip what lies past its last
+         * rather than leave the loop: the compiler unrolls a loop with an early exit whole only up
+         * to 8 steps */
 #pragma unroll
-        for (int ch = 0; ch < SC; ch++) {
-            if (ch >= nc)
+        for (int e = 0; e < NP * SC; e++) {
+            if (NP == 1 && e >= nc)
                 break;
+            if (NP == 2 && e >= 2 * nc)
+                continue;
+            const int pe = NP == 2 && e >= nc ? 1 : 0, ch = e - pe * nc;
+            if (NP == 2 && e == nc) { /* product 1's ranges from here: its sums in acc, product 0's aside */
+                const f32x4 a = acc;
+                acc = oth;
+                oth = a;
+            }
+            const uint16_t *dl = dls + (NP == 2 && pe ? DL : 0);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int p = 0; p < KP; p++) {
                 const int c = c00 + ch * KP + p;
                 const bool ok0 = live && c < np, ok1 = live && 2 * c + 1 < nb; /* block 2c, block 2c+1 */
-                const uint4 qq = q[ch & 1][p];
+                const uint4 qq = q[e & 1][p];
                 /* A block past the matrix (its weights loaded from a clamped index) needs no masking:
                  * its x limbs in LDS are zero, and a bf16 weight is finite, so its MFMAs give exactly
                  * 0; its scale is zeroed below, in case the clamped block's scale is not finite.
@@ -414,7 +446,7 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
                 const auto s13 = __builtin_amdgcn_permlane32_swap(qq.y, qq.w, false, false);
                 const bf16x8 wb[2] = {q8_bf16(s02[0], s13[0]), q8_bf16(s02[1], s13[1])};
                 const int bs = 2 * (ch * KP + p), lr = wave * 16 + n; /* block 2c in the segment, the lane's row in the workgroup */
-                const float d0 = q8_half(dls[lr * DP + bs]), d1 = q8_half(dls[lr * DP + bs + 1]);
+                const float d0 = q8_half(dl[lr * DP + bs]), d1 = q8_half(dl[lr * DP + bs + 1]);
                 const float d[2] = {ok0 ? d0 : 0.0f, ok1 ? d1 : 0.0f};
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
@@ -428,15 +460,22 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (ch + 2 < SC) {
-                const int nx = ch + 2 < nc ? ch + 2 : nc - 1;
+            if (e + 2 < NP * SC) {
+                int pn;
+                const int nx = step(e + 2, pn);
+                const uint8_t *wn = NP == 2 && pn ? wt[NP - 1] : wt[0];
 #pragma unroll
                 for (int p = 0; p < KP; p++) {
                     int c = c00 + nx * KP + p;
                     c = c < np ? c : np - 1;
-                    q[ch & 1][p] = *(const uint4 *)(wt + 64L * c + woff);
+                    q[e & 1][p] = *(const uint4 *)(wn + 64L * c + woff);
                 }
             }
+        }
+        if (NP == 2) { /* product 0's sums back in acc for the next segment */
+            const f32x4 a = acc;
+            acc = oth;
+            oth = a;
         }
         __syncthreads(); /* every wave done with the segment's LDS before the next segment writes it */
     }
@@ -445,14 +484,18 @@ __device__ __forceinline__ void xres_body(const uint8_t *w, long rows, long cols
         return;
     const long tp = (t + 15) / 16 * 16;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const long tok = 4 * kq + j;
-        if (ks == 1) {
-            const long i = tok * rows + rt0 * 16 + n;
-            if (tok < t)
-                y[i] = res ? res[i] + acc[j] : acc[j];
-        } else if (tok < tp) {
-            part[((long)split * tp + tok) * rows + rt0 * 16 + n] = acc[j];
+    for (int pp = 0; pp < NP; pp++) {
+        const f32x4 a = pp ? oth : acc;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const long tok = 4 * kq + j;
+            if (ks == 1) {
+                const long i = tok * rows + rt0 * 16 + n;
+                if (tok < t)
+                    y[pp][i] = res ? res[i] + a[j] : a[j];
+            } else if (tok < tp) {
+                part[pp][((long)split * tp + tok) * rows + rt0 * 16 + n] = a[j];
+            }
         }
     }
 }
@@ -461,7 +504,9 @@ template <int KP, int NW, int SC>
 __global__ __launch_bounds__(64 * NW) void gemm_xres(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
                                                      float *part, float *y, const float *res)
 {
-    xres_body<KP, NW, SC>(w, rows, cols, x, x_stride, t, ks, cps, part, y, res, blockIdx.x);
+    const uint8_t *const wv[1] = {w};
+    float *const pv[1] = {part}, *const yv[1] = {y};
+    xres_body<KP, NW, SC>(wv, rows, cols, x, x_stride, t, ks, cps, pv, yv, res, blockIdx.x);
 }
 
 /* A round of products that share x (and t <= 16) as one launch: workgroup b belongs to product p
@@ -475,8 +520,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_xres_round(q8_gemm_round r, long
     for (int k = 1; k < Q8_ROUND_MAX; k++)
         if (k < r.n && (long)blockIdx.x >= r.start[k])
             p = k;
-    xres_body<KP, NW, SC>((const uint8_t *)r.w[p], r.rows[p], cols, x, x_stride, t, r.ks[p], r.cps[p], r.out[p], r.out[p], nullptr,
-                          (unsigned)(blockIdx.x - r.start[p]));
+    const uint8_t *const wv[1] = {(const uint8_t *)r.w[p]};
+    float *const ov[1] = {r.out[p]};
+    xres_body<KP, NW, SC>(wv, r.rows[p], cols, x, x_stride, t, r.ks[p], r.cps[p], ov, ov, nullptr, (unsigned)(blockIdx.x - r.start[p]));
+}
+
+/* The two products of a round of one shape (the FFN's gate and up) in one workgroup a tile and
+ * split: the split's x limbs go to LDS once for both, and the waves stream product 0's ranges,
+ * then product 1's, through the same two register sets (product 1's first ranges in flight during
+ * product 0's last). Each product's sums are those of its own launch, in the same order; the
+ * workgroups of the pair are half those of the two products' own grids. */
+template <int KP, int NW, int SC>
+__global__ __launch_bounds__(64 * NW) void gemm_xres_pair(q8_gemm_round r, long cols, const float *x, long x_stride, long t)
+{
+    const uint8_t *const wv[2] = {(const uint8_t *)r.w[0], (const uint8_t *)r.w[1]};
+    float *const ov[2] = {r.out[0], r.out[1]};
+    xres_body<KP, NW, SC, 2>(wv, r.rows[0], cols, x, x_stride, t, r.ks[0], r.cps[0], ov, ov, nullptr, blockIdx.x);
 }
 
 /* The floor of gemm_xres: its grid, segments, barriers and loads (x, the scales, the weights
@@ -841,8 +900,21 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
      * wave count of its largest product, then every product's sums. The waves a workgroup only
      * decide which rows a workgroup streams; each product keeps its own K split, and so the bits
      * of its own launch (the attention layer's K and V, 1024 x 4096, plan 12 waves alone and run
-     * at Q's 16 in its round) */
+     * at Q's 16 in its round). Two products of one shape on the x-resident kernel (the FFN's gate
+     * and up) run as a pair: one workgroup a tile and split for both, x staged once */
     bool launched[Q8_ROUND_MAX] = {};
+    if (n == 2 && pl[0].xres && pl[1].xres && rows[0] == rows[1] && pl[0].c.nw == pl[1].c.nw && all.ks[0] == all.ks[1] &&
+        all.cps[0] == all.cps[1]) {
+        const int nw = pl[0].c.nw;
+        const dim3 grid((unsigned)((rows[0] + 16L * nw - 1) / (16L * nw) * all.ks[0]));
+        if (nw == 12)
+            Q8_LAUNCH(q8_time_name("gemm_xres_pair", 3, XRES_KP, 12, XRES_SC), (gemm_xres_pair<XRES_KP, 12, XRES_SC>), grid, dim3(64 * 12), s, all,
+                      cols, x, x_stride, t);
+        else
+            Q8_LAUNCH(q8_time_name("gemm_xres_pair", 3, XRES_KP, 16, XRES_SC), (gemm_xres_pair<XRES_KP, 16, XRES_SC>), grid, dim3(64 * 16), s, all,
+                      cols, x, x_stride, t);
+        launched[0] = launched[1] = true;
+    }
     for (int p0 = 0; p0 < n; p0++) {
         if (launched[p0])
             continue;
