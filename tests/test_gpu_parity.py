@@ -748,6 +748,51 @@ def test_random_shapes_every_path(rt, oracle, case):
         rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
 
 
+def random_round_cases(n=14, seed=4242):
+    """Seeded rounds: 2 to 8 products sharing x, rows 16..1536 and K 32..4096 columns at random, every
+    third case of one shape (two products of one shape at 5..16 tokens run as a pair), at 1 to 70
+    tokens (decode rounds, x-resident, streaming, and 64-token chunks with a short last one)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        k = 2 if i % 3 == 0 else int(rng.integers(2, 9))
+        cols = 32 * int(rng.integers(1, 129))
+        rows = [16 * int(rng.integers(1, 97)) for _ in range(k)]
+        if i % 3 == 0:
+            rows = [rows[0]] * k
+        t = int(rng.choice([1, 3, 4, 5, 8, 13, 16, 17, 29, 40, 64, 66, 70]))
+        out.append((i, tuple(rows), cols, t))
+    return out
+
+
+@pytest.mark.parametrize("case", random_round_cases(), ids=lambda c: f"{len(c[1])}x{c[1][0]}x{c[2]}t{c[3]}")
+def test_random_rounds_equal_singles(rt, oracle, case):
+    """rt_gemv_round_dev on seeded random rounds: every product's y has the bits of its own
+    rt_gemm_dev at every token count (one launch for the products, a pair for two of one shape,
+    the decode round below 5 tokens) and meets the parity bar against F64."""
+    i, shapes, cols, t = case
+    n = len(shapes)
+    rng = np.random.default_rng(9500 + i)
+    mats = [synth.q8_rows(rng, r, cols) for r in shapes]
+    x = synth.x_f32(rng, t, cols)
+    say("random round", shapes, cols, t)
+    ws = [rt.upload(m, r, cols) for m, r in zip(mats, shapes)]
+    try:
+        singles = [gpu_gemm(rt, m, r, cols, x, w=w) for m, r, w in zip(mats, shapes, ws)]
+        with Dev(rt) as d:
+            dx = d.put(x)
+            ys = [d.empty(4 * t * r) for r in shapes]
+            W, R, Y = (c.c_void_p * n)(*ws), (c.c_long * n)(*shapes), (c.c_void_p * n)(*ys)
+            rt.lib.rt_gemv_round_dev(rt.R, n, W, R, cols, c.c_void_p(dx), cols, t, Y)
+            got = [d.get(p, (t, r), np.float32) for p, r in zip(ys, shapes)]
+        for g, s1, m, r in zip(got, singles, mats, shapes):
+            assert np.array_equal(g.view(np.uint32), s1.view(np.uint32)), r
+            assert_parity(g, oracle.gemm_f64(m, r, cols, x), f"round {r}x{cols} t={t}")
+    finally:
+        for w in ws:
+            rt.lib.rt_q8_free(rt.R, c.c_void_p(w))
+
+
 INVARIANT_CASES = [(256, 1024, 1), (512, 2048, 3), (1024, 4096, 16), (768, 1056, 9), (512, 4096, 40)]
 
 
