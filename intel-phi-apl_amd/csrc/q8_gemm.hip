@@ -23,7 +23,15 @@
  *               MFMAs. With K split over ks workgroups, each writes a partial;
  *   gemm_xres   the same for one token tile (t <= 16), with the split's x limbs and scales put in
  *               LDS once, so the weights stream with no per-range wait or barrier;
- *   gemm_sum    adds the ks partials in split order: the same order every run, deterministic. */
+ *   gemm_sum    adds the ks partials in split order: the same order every run, deterministic;
+ *   gemm_xres_round, gemm_mfma_round
+ *               a round of products sharing x in one launch, each product on its own K split;
+ *   gemm_xres_pair
+ *               two products of one shape at t <= 16 (the FFN's gate and up): a workgroup stages
+ *               x once and streams both products' rows of its tile and split;
+ *   gemm_sum_round, gemm_swiglu_round
+ *               every product's partials of a round in split order (the fused pair's with its
+ *               SwiGLU). */
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
