@@ -423,7 +423,7 @@ def deltanet_round(b):
 
 
 def prompt_rounds(b):
-    """At M = 16 and 64 tokens (a prompt chunk, a speculative verify), three rounds of products that
+    """At M = 16, 40 and 64 tokens (prompt chunks, a speculative verify), three rounds of products that
     share x, over 32 layers of distinct weights, each recorded as a graph: every product launched
     alone (its matrix-core kernel and its partial sum) against one round a layer
     (rt_gemv_round_dev: one launch for the products, one launch of the sums). The 9B DeltaNet quartet (qwen35.apl:93-96), the attention layer's Q, K and V
@@ -431,7 +431,7 @@ def prompt_rounds(b):
     pair SiLU(X Wg^T) * (X Wu^T) (rt_gemv_swiglu_dev: the round with the SwiGLU in its sums' launch).
     GB/s counts the weights' bytes."""
     out = {}
-    for m, name, shapes in [(m, name, shapes) for m in (16, 64) for name, shapes in
+    for m, name, shapes in [(m, name, shapes) for m in (16, 40, 64) for name, shapes in
                             (("deltanet_quartet", [8192, 4096, 32, 32]), ("attention_qkv", [8192, 1024, 1024]), ("ffn_gate_up", [FFN, FFN]))]:
         n = len(shapes)
         layers = [[b.matrix(r, HIDDEN) for r in shapes] for _ in range(LAYERS)]

@@ -258,7 +258,8 @@ long q8_gemm_part_floats(long rows, long cols, long t, q8_gemm_opts o);
 /* A round of products sharing x at 1 <= t <= 64 tokens (one 64-token chunk of a longer X, so the
  * last chunk of one with 65 to 68 tokens holds fewer than 5; rounds of fewer than 5 tokens in all
  * run on the decode kernel): one matrix-core launch for the products (the x-resident kernel at
- * t <= 16, the streaming one above, at the largest product's wave count) and one launch of every
+ * t <= 16, the streaming one above, at the largest product's wave count; two products of one shape
+ * as a pair kernel where one is built for the configuration) and one launch of every
  * product's partial sums, each product on its own K split (its single launch's bits, as
  * q8_launch_gemm_mfma's at any t): 0, or -1 (nothing launched: the partials need more than part_cap floats
  * of part, q8_gemm_round_part_floats; the caller runs them one by one). pair_y != NULL: the fused

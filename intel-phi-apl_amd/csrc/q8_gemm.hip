@@ -63,7 +63,7 @@ __device__ __forceinline__ void mfma_block(const bf16x8 (&wb)[RT], const float (
 #define GEMM_CHUNK 8
 
 /* The loads of one range of KP pairs, held in registers from issue to commit. */
-template <int MT, int RT, int KP, int NW>
+template <int MT, int RT, int KP, int NW, int NP = 1>
 struct gemm_stage {
     static constexpr int XS = MT * 2 * KP * 64;               /* x lane slots: 8 values of one token each */
     static constexpr int XR = (XS + 64 * NW - 1) / (64 * NW); /* of them a thread */
@@ -71,8 +71,8 @@ struct gemm_stage {
     static constexpr int DR = (DN + 64 * NW - 1) / (64 * NW);
     float4 xr[XR][2];
     bool xin[XR];
-    uint16_t dr[DR];
-    uint4 q[KP][RT];
+    uint16_t dr[NP][DR]; /* every product's scales */
+    uint4 q[NP][KP][RT];  /* every product's weights */
 };
 
 /* A workgroup of NW waves owns NW*RT row tiles of 16 rows (wave w: tiles [w*RT, +RT)), MT token
@@ -84,15 +84,15 @@ struct gemm_stage {
  * the MFMAs of range ch, so a workgroup streams its K slice with one range always in flight.
  * The ks workgroups of a row tile write partials that gemm_sum adds in split order. blk: the
  * workgroup's index in the product's grid along x (tile blk / ks, split blk % ks). */
-template <int MT, int RT, int KP, int NW>
-__device__ __forceinline__ void mfma_body(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
-                                          float *part, float *y, const float *res, unsigned blk)
+template <int MT, int RT, int KP, int NW, int NP = 1>
+__device__ __forceinline__ void mfma_body(const uint8_t *const (&w)[NP], long rows, long cols, const float *x, long x_stride, long t, int ks,
+                                          int cps, float *const (&part)[NP], float *const (&y)[NP], const float *res, unsigned blk)
 {
-    typedef gemm_stage<MT, RT, KP, NW> stage;
+    typedef gemm_stage<MT, RT, KP, NW, NP> stage;
     constexpr int XS = stage::XS, XR = stage::XR, DN = stage::DN, DR = stage::DR;
     constexpr int XN = MT * 2 * KP * 192; /* uint4 of x limbs in a range */
     __shared__ uint4 xls[2][XN];          /* two ranges: [tt][block in range][limb][lane] */
-    __shared__ uint16_t dls[2][DN];       /* two ranges: [row of the workgroup][block in range] */
+    __shared__ uint16_t dls[2][NP * DN];  /* two ranges: [product][row of the workgroup][block in range] */
     const int lane = threadIdx.x & 63;
     /* the wave's index, uniform (see gemm_xres) */
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -133,19 +133,23 @@ __device__ __forceinline__ void mfma_body(const uint8_t *w, long rows, long cols
                 row = row < rows ? row : rows - 1;
                 int b = 2 * c0 + i % (2 * KP);
                 b = b < nb ? b : nb - 1;
-                S.dr[k] = ((const uint16_t *)(w + q8s_row_d(row, cols)))[b];
+#pragma unroll
+                for (int pp = 0; pp < NP; pp++)
+                    S.dr[pp][k] = ((const uint16_t *)(w[pp] + q8s_row_d(row, cols)))[b];
             }
         }
 #pragma unroll
-        for (int p = 0; p < KP; p++) {
-            const int c = c0 + p < np ? c0 + p : np - 1;
+        for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-                /* the row tile at a uniform base, the lane's row and 16 bytes at a 32-bit offset */
-                const uint8_t *wt = w + q8s_row_q(live_r(r) ? (rt0 + r) * 16 : 0, cols) + 64L * c;
-                S.q[p][r] = *(const uint4 *)(wt + (unsigned)(n * cols + 16 * kq));
+            for (int p = 0; p < KP; p++) {
+                const int c = c0 + p < np ? c0 + p : np - 1;
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    /* the row tile at a uniform base, the lane's row and 16 bytes at a 32-bit offset */
+                    const uint8_t *wt = w[pp] + q8s_row_q(live_r(r) ? (rt0 + r) * 16 : 0, cols) + 64L * c;
+                    S.q[pp][p][r] = *(const uint4 *)(wt + (unsigned)(n * cols + 16 * kq));
+                }
             }
-        }
     };
     /* the range's x limbs and scales into LDS buffer bf */
     auto commit = [&](const stage &S, int bf) {
@@ -165,18 +169,22 @@ __device__ __forceinline__ void mfma_body(const uint8_t *w, long rows, long cols
             }
         }
 #pragma unroll
-        for (int k = 0; k < DR; k++) {
-            const int i = (int)threadIdx.x + 64 * NW * k;
-            if (DN % (64 * NW) == 0 || i < DN)
-                dl[i] = S.dr[k];
-        }
+        for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+            for (int k = 0; k < DR; k++) {
+                const int i = (int)threadIdx.x + 64 * NW * k;
+                if (DN % (64 * NW) == 0 || i < DN)
+                    dl[pp * DN + i] = S.dr[pp][k];
+            }
     };
-    f32x4 acc[RT][MT];
+    f32x4 acc[NP][RT][MT];
 #pragma unroll
-    for (int r = 0; r < RT; r++)
+    for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-        for (int m = 0; m < MT; m++)
-            acc[r][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                acc[pp][r][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     /* the MFMAs of the range starting at pair c0, from LDS buffer bf and the stage's weights */
     auto compute = [&](const stage &S, int bf, int c0) {
         const uint4 *xl = xls[bf];
@@ -185,31 +193,56 @@ __device__ __forceinline__ void mfma_body(const uint8_t *w, long rows, long cols
         for (int p = 0; p < KP; p++) {
             const int c = c0 + p;
             const bool ok0 = c < np, ok1 = 2 * c + 1 < nb; /* block 2c, block 2c+1 */
-            bf16x8 wb[2][RT];
-            float d[2][RT];
+            bf16x8 wb[NP][2][RT];
+            float d[NP][2][RT];
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-                /* a block past the matrix needs no masking: its x limbs in LDS are zero and a bf16 weight is
-                 * finite, so its MFMAs give exactly 0 (its scale is zeroed below). Lanes 0-31 hold block 2c,
-                 * 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
-                const auto s02 = __builtin_amdgcn_permlane32_swap(S.q[p][r].x, S.q[p][r].z, false, false);
-                const auto s13 = __builtin_amdgcn_permlane32_swap(S.q[p][r].y, S.q[p][r].w, false, false);
-                wb[0][r] = q8_bf16(s02[0], s13[0]);
-                wb[1][r] = q8_bf16(s02[1], s13[1]);
-                const int lr = (wave * RT + r) * 16 + n; /* the lane's row in the workgroup */
-                const float d0 = q8_half(dl[lr * 2 * KP + 2 * p]), d1 = q8_half(dl[lr * 2 * KP + 2 * p + 1]);
-                d[0][r] = ok0 && live_r(r) ? d0 : 0.0f;
-                d[1][r] = ok1 && live_r(r) ? d1 : 0.0f;
-            }
+            for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    /* a block past the matrix needs no masking: its x limbs in LDS are zero and a bf16 weight is
+                     * finite, so its MFMAs give exactly 0 (its scale is zeroed below). Lanes 0-31 hold block 2c,
+                     * 32-63 block 2c+1: trade dwords 0<->2 and 1<->3 across the halves */
+                    const auto s02 = __builtin_amdgcn_permlane32_swap(S.q[pp][p][r].x, S.q[pp][p][r].z, false, false);
+                    const auto s13 = __builtin_amdgcn_permlane32_swap(S.q[pp][p][r].y, S.q[pp][p][r].w, false, false);
+                    wb[pp][0][r] = q8_bf16(s02[0], s13[0]);
+                    wb[pp][1][r] = q8_bf16(s02[1], s13[1]);
+                    const int lr = (wave * RT + r) * 16 + n; /* the lane's row in the workgroup */
+                    const float d0 = q8_half(dl[pp * DN + lr * 2 * KP + 2 * p]), d1 = q8_half(dl[pp * DN + lr * 2 * KP + 2 * p + 1]);
+                    d[pp][0][r] = ok0 && live_r(r) ? d0 : 0.0f;
+                    d[pp][1][r] = ok1 && live_r(r) ? d1 : 0.0f;
+                }
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                uint4 xa[MT][3];
+                if constexpr (NP == 1) {
+                    uint4 xa[MT][3];
 #pragma unroll
-                for (int m = 0; m < MT; m++)
+                    for (int m = 0; m < MT; m++)
 #pragma unroll
-                    for (int l = 0; l < 3; l++)
-                        xa[m][l] = xl[((m * 2 * KP + 2 * p + h) * 3 + l) * 64 + lane];
-                mfma_block<MT, RT>(wb[h], d[h], xa, acc);
+                        for (int l = 0; l < 3; l++)
+                            xa[m][l] = xl[((m * 2 * KP + 2 * p + h) * 3 + l) * 64 + lane];
+                    mfma_block<MT, RT>(wb[0][h], d[0][h], xa, acc[0]);
+                } else {
+                    /* a pair: one token tile's limbs at a time (12 registers, not 12 per tile), read once
+                     * for both products' MFMAs, in the order of mfma_block for each product */
+#pragma unroll
+                    for (int m = 0; m < MT; m++) {
+                        uint4 xa[1][3];
+#pragma unroll
+                        for (int l = 0; l < 3; l++)
+                            xa[0][l] = xl[((m * 2 * KP + 2 * p + h) * 3 + l) * 64 + lane];
+#pragma unroll
+                        for (int pp = 0; pp < NP; pp++) {
+                            f32x4 a1[RT][1];
+#pragma unroll
+                            for (int r = 0; r < RT; r++)
+                                a1[r][0] = acc[pp][r][m];
+                            mfma_block<1, RT>(wb[pp][h], d[pp][h], xa, a1);
+#pragma unroll
+                            for (int r = 0; r < RT; r++)
+                                acc[pp][r][m] = a1[r][0];
+                        }
+                    }
+                }
             }
         }
     };
@@ -260,30 +293,34 @@ __device__ __forceinline__ void mfma_body(const uint8_t *w, long rows, long cols
         return;
     const long tp = (t + 15) / 16 * 16;
 #pragma unroll
-    for (int r = 0; r < RT; r++) {
-        if (!live_r(r))
-            continue;
+    for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-        for (int m = 0; m < MT; m++)
+        for (int r = 0; r < RT; r++) {
+            if (!live_r(r))
+                continue;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const long tok = 16 * (tt0 + m) + 4 * kq + j;
-                if (ks == 1) {
-                    const long i = tok * rows + (rt0 + r) * 16 + n;
-                    if (tok < t)
-                        y[i] = res ? res[i] + acc[r][m][j] : acc[r][m][j];
-                } else if (tok < tp) {
-                    part[((long)split * tp + tok) * rows + (rt0 + r) * 16 + n] = acc[r][m][j];
+            for (int m = 0; m < MT; m++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const long tok = 16 * (tt0 + m) + 4 * kq + j;
+                    if (ks == 1) {
+                        const long i = tok * rows + (rt0 + r) * 16 + n;
+                        if (tok < t)
+                            y[pp][i] = res ? res[i] + acc[pp][r][m][j] : acc[pp][r][m][j];
+                    } else if (tok < tp) {
+                        part[pp][((long)split * tp + tok) * rows + (rt0 + r) * 16 + n] = acc[pp][r][m][j];
+                    }
                 }
-            }
-    }
+        }
 }
 
 template <int MT, int RT, int KP, int NW>
 __global__ __launch_bounds__(64 * NW) void gemm_mfma(const uint8_t *w, long rows, long cols, const float *x, long x_stride, long t, int ks, int cps,
                                                      float *part, float *y, const float *res)
 {
-    mfma_body<MT, RT, KP, NW>(w, rows, cols, x, x_stride, t, ks, cps, part, y, res, blockIdx.x);
+    const uint8_t *const wv[1] = {w};
+    float *const pv[1] = {part}, *const yv[1] = {y};
+    mfma_body<MT, RT, KP, NW>(wv, rows, cols, x, x_stride, t, ks, cps, pv, yv, res, blockIdx.x);
 }
 
 /* A round of products sharing x (17 <= t <= 64) as one launch: workgroup (b, g) runs position
@@ -296,8 +333,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_mfma_round(q8_gemm_round r, long
     for (int k = 1; k < Q8_ROUND_MAX; k++)
         if (k < r.n && (long)blockIdx.x >= r.start[k])
             p = k;
-    mfma_body<MT, RT, KP, NW>((const uint8_t *)r.w[p], r.rows[p], cols, x, x_stride, t, r.ks[p], r.cps[p], r.out[p], r.out[p], nullptr,
-                              (unsigned)(blockIdx.x - r.start[p]));
+    const uint8_t *const wv[1] = {(const uint8_t *)r.w[p]};
+    float *const ov[1] = {r.out[p]};
+    mfma_body<MT, RT, KP, NW>(wv, r.rows[p], cols, x, x_stride, t, r.ks[p], r.cps[p], ov, ov, nullptr, (unsigned)(blockIdx.x - r.start[p]));
+}
+
+/* The two products of a round of one shape (the FFN's gate and up) at 17 <= t <= 64: each range's
+ * x goes to LDS once for both, and each wave reads a block's x limbs once for both products'
+ * MFMAs. Each product's sums are those of its own launch, in the same order. */
+template <int MT, int RT, int KP, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_mfma_pair(q8_gemm_round r, long cols, const float *x, long x_stride, long t)
+{
+    const uint8_t *const wv[2] = {(const uint8_t *)r.w[0], (const uint8_t *)r.w[1]};
+    float *const ov[2] = {r.out[0], r.out[1]};
+    mfma_body<MT, RT, KP, NW, 2>(wv, r.rows[0], cols, x, x_stride, t, r.ks[0], r.cps[0], ov, ov, nullptr, blockIdx.x);
 }
 
 /* One token tile (t <= 16) with x resident in LDS. A workgroup of NW waves owns NW row tiles
@@ -737,6 +786,14 @@ struct gemm_cfg {
  * units idle (nw_of); the 12-wave instances of one token tile are the streaming twins of the
  * x-resident kernel's */
 #define GEMM_CFGS(X) X(1, 1, 2, 16) X(2, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 16) X(1, 1, 2, 12) X(3, 1, 2, 12) X(4, 1, 2, 12)
+/* the streaming configurations that also run as a pair (two products of one shape sharing each
+ * range's x and each block's x limb reads): those whose pair kernel needs no more registers than
+ * leave the single kernel's waves a SIMD and spills none. 3 token tiles on 12 waves: 152
+ * registers, and a round of the 9B gate and up 49.5 / 51.6 us a layer at 40 / 48 tokens against
+ * 54.0 / 56.4 as two products. Measured and left out: 2 tiles on 8 waves (132 registers, half
+ * the workgroups a CU: 52.3 / 54.9 against 43.5 / 47.0 us at 24 / 32 tokens), 4 tiles on 12
+ * waves (18 registers spilled: 82.3 against 68.7 us at 64), and every 16-wave one (spills). */
+#define GEMM_PAIR_CFGS(X) X(3, 1, 2, 12)
 
 /* the x-resident kernel for one token tile: 2-pair ranges, 16 or 12 waves, segments of 8 ranges
  * (x limbs 96 KiB and scales 13-17 KiB of LDS: one workgroup a CU) */
@@ -911,17 +968,32 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
      * at Q's 16 in its round). Two products of one shape on the x-resident kernel (the FFN's gate
      * and up) run as a pair: one workgroup a tile and split for both, x staged once */
     bool launched[Q8_ROUND_MAX] = {};
-    if (n == 2 && pl[0].xres && pl[1].xres && rows[0] == rows[1] && pl[0].c.nw == pl[1].c.nw && all.ks[0] == all.ks[1] &&
-        all.cps[0] == all.cps[1]) {
-        const int nw = pl[0].c.nw;
-        const dim3 grid((unsigned)((rows[0] + 16L * nw - 1) / (16L * nw) * all.ks[0]));
-        if (nw == 12)
-            Q8_LAUNCH(q8_time_name("gemm_xres_pair", 3, XRES_KP, 12, XRES_SC), (gemm_xres_pair<XRES_KP, 12, XRES_SC>), grid, dim3(64 * 12), s, all,
-                      cols, x, x_stride, t);
-        else
-            Q8_LAUNCH(q8_time_name("gemm_xres_pair", 3, XRES_KP, 16, XRES_SC), (gemm_xres_pair<XRES_KP, 16, XRES_SC>), grid, dim3(64 * 16), s, all,
-                      cols, x, x_stride, t);
-        launched[0] = launched[1] = true;
+    const gemm_cfg &q0 = pl[0].c, &q1 = pl[1].c;
+    if (n == 2 && rows[0] == rows[1] && pl[0].xres == pl[1].xres && q0.mg == q1.mg && q0.rt == q1.rt && q0.kp == q1.kp && q0.nw == q1.nw &&
+        all.ks[0] == all.ks[1] && all.cps[0] == all.cps[1]) {
+        const int nw = q0.nw, rowsper = 16 * nw * (pl[0].xres ? 1 : q0.rt);
+        const unsigned wgs = (unsigned)((rows[0] + rowsper - 1) / rowsper * all.ks[0]);
+        bool ok = false;
+        if (pl[0].xres) {
+            if (nw == 12)
+                Q8_LAUNCH(q8_time_name("gemm_xres_pair", 3, XRES_KP, 12, XRES_SC), (gemm_xres_pair<XRES_KP, 12, XRES_SC>), dim3(wgs), dim3(64 * 12), s,
+                          all, cols, x, x_stride, t);
+            else
+                Q8_LAUNCH(q8_time_name("gemm_xres_pair", 3, XRES_KP, 16, XRES_SC), (gemm_xres_pair<XRES_KP, 16, XRES_SC>), dim3(wgs), dim3(64 * 16), s,
+                          all, cols, x, x_stride, t);
+            ok = true;
+        } else {
+            const unsigned groups = (unsigned)(((t + 15) / 16 + q0.mg - 1) / q0.mg);
+#define GP(G, R, P, N)                                                                                                 \
+    if (!ok && q0.mg == G && q0.rt == R && q0.kp == P && nw == N) {                                                    \
+        Q8_LAUNCH(q8_time_name("gemm_mfma_pair", 4, G, R, P, N), (gemm_mfma_pair<G, R, P, N>), dim3(wgs, groups), dim3(64 * N), s, all, cols, x,  \
+                  x_stride, t);                                                                                        \
+        ok = true;                                                                                                     \
+    }
+            GEMM_PAIR_CFGS(GP)
+#undef GP
+        }
+        launched[0] = launched[1] = ok;
     }
     for (int p0 = 0; p0 < n; p0++) {
         if (launched[p0])
