@@ -787,13 +787,17 @@ struct gemm_cfg {
  * x-resident kernel's */
 #define GEMM_CFGS(X) X(1, 1, 2, 16) X(2, 1, 2, 8) X(3, 1, 2, 16) X(4, 1, 2, 16) X(1, 1, 2, 12) X(3, 1, 2, 12) X(4, 1, 2, 12)
 /* the streaming configurations that also run as a pair (two products of one shape sharing each
- * range's x and each block's x limb reads): those whose pair kernel needs no more registers than
- * leave the single kernel's waves a SIMD and spills none. 3 token tiles on 12 waves: 152
- * registers, and a round of the 9B gate and up 49.5 / 51.6 us a layer at 40 / 48 tokens against
- * 54.0 / 56.4 as two products. Measured and left out: 2 tiles on 8 waves (132 registers, half
- * the workgroups a CU: 52.3 / 54.9 against 43.5 / 47.0 us at 24 / 32 tokens), 4 tiles on 12
- * waves (18 registers spilled: 82.3 against 68.7 us at 64), and every 16-wave one (spills). */
-#define GEMM_PAIR_CFGS(X) X(3, 1, 2, 12)
+ * range's x and each block's x limb reads), as X(MG, RT, KP, NW, the pair's KP): those whose pair
+ * kernel spills nothing and leaves the single kernel's waves a SIMD. The pair may stream ranges of
+ * fewer pairs than the plan's (the split's cps ranges of KP pairs as KP / PK times as many ranges:
+ * the same blocks in the same order, so the same bits), which halves the weights and x a stage
+ * holds. A round of the 9B gate and up: 3 token tiles on 12 waves (152 registers) 49.5-50.5 /
+ * 51.6-52.5 us a layer at 40 / 48 tokens against 54.0-55.5 / 56.4-57.8 as two products; 4 tiles
+ * on 12 waves in ranges of one pair (112 registers) 67.2 against 70.2 us at 64 (in ranges of two
+ * pairs it spilled 18 registers: 82.3 against 68.7). Measured and left out: 2 tiles on 8 waves,
+ * 52.3-55.6 / 54.9-58.7 against 43.5-44.4 / 47.0-47.5 us at 24 / 32 tokens in ranges of two pairs
+ * (132 registers, half the workgroups a CU) or one (113), and every 16-wave one (spills). */
+#define GEMM_PAIR_CFGS(X) X(3, 1, 2, 12, 2) X(4, 1, 2, 12, 1)
 
 /* the x-resident kernel for one token tile: 2-pair ranges, 16 or 12 waves, segments of 8 ranges
  * (x limbs 96 KiB and scales 13-17 KiB of LDS: one workgroup a CU) */
@@ -984,10 +988,13 @@ int q8_launch_gemm_round(q8_stream_t stream, int n, const void *const *w, const 
             ok = true;
         } else {
             const unsigned groups = (unsigned)(((t + 15) / 16 + q0.mg - 1) / q0.mg);
-#define GP(G, R, P, N)                                                                                                 \
+#define GP(G, R, P, N, PK)                                                                                             \
     if (!ok && q0.mg == G && q0.rt == R && q0.kp == P && nw == N) {                                                    \
-        Q8_LAUNCH(q8_time_name("gemm_mfma_pair", 4, G, R, P, N), (gemm_mfma_pair<G, R, P, N>), dim3(wgs, groups), dim3(64 * N), s, all, cols, x,  \
-                  x_stride, t);                                                                                        \
+        q8_gemm_round pr = all; /* ranges of PK pairs: the split's cps ranges of P pairs as P / PK times as many */    \
+        pr.cps[0] *= P / PK;                                                                                           \
+        pr.cps[1] *= P / PK;                                                                                           \
+        Q8_LAUNCH(q8_time_name("gemm_mfma_pair", 4, G, R, PK, N), (gemm_mfma_pair<G, R, PK, N>), dim3(wgs, groups), dim3(64 * N), s, pr, cols,  \
+                  x, x_stride, t);                                                                                     \
         ok = true;                                                                                                     \
     }
             GEMM_PAIR_CFGS(GP)

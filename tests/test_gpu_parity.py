@@ -434,9 +434,10 @@ def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
             got = [d.get(p, (t, r), np.float32) for p, r in zip(ys, shapes)]
         say("round", shapes, t, kname)
         pair = n == 2 and shapes[0] == shapes[1]
-        # the streaming pair runs on 3 token tiles (33..48 tokens) of 12 waves, which 12288 rows plan
+        # the streaming pair runs on 3 and 4 token tiles (33..64 tokens, the first chunk of 65..70) of
+        # 12 waves, which 12288 rows plan
         assert kname.startswith(("gemm_xres_pair<" if pair else "gemm_xres_round<") if t <= 16 else
-                                ("gemm_mfma_pair<" if pair and 33 <= t <= 48 else "gemm_mfma_round<"))
+                                ("gemm_mfma_pair<" if pair and t >= 33 else "gemm_mfma_round<"))
         for g, s1, m, r in zip(got, singles, mats, shapes):
             assert np.array_equal(g.view(np.uint32), s1.view(np.uint32)), r
             assert_parity(g, oracle.gemm_f64(m, r, cols, x), f"round {r}x{cols} t={t}")
@@ -450,9 +451,10 @@ def test_matrix_core_round_equals_singles(rt, oracle, t, shapes):
 def test_pair_round_equals_singles(rt, oracle, rows, cols, ks):
     """Two products of one shape (the FFN's gate and up, qwen35.apl:125) run as one pair kernel. At
     5 to 16 tokens a workgroup stages x once and streams product 0's ranges, then product 1's, with
-    product 1's first loads issued during product 0's last ranges; at 40 tokens on the 12-wave kernel
-    each range's x is staged once and each block's x limbs read once for both products' MFMAs (64
-    tokens, and 16 waves, run the round kernel). Each product's
+    product 1's first loads issued during product 0's last ranges; at 40 and 64 tokens on the 12-wave
+    kernels each range's x is staged once and each block's x limbs read once for both products'
+    MFMAs (at 64 in ranges of one block pair: the split as twice as many ranges; 16 waves run the
+    round kernel). Each product's
     bits are those of its own rt_gemm_dev, at the planner's K split and at forced splits of 1 and
     3, which give several segments a split, segments of an odd number of ranges and of one range
     (the prefetch crosses into product 1 at once); 12288 x 4096 takes the 12-wave kernels, 4096 x
@@ -474,11 +476,9 @@ def test_pair_round_equals_singles(rt, oracle, rows, cols, ks):
                 say("pair round", rows, cols, "t", t, "ks", ks or "planned", kname)
                 if t <= 16:
                     assert kname.startswith("gemm_xres_pair<"), kname
-                elif t == 40:  # the streaming pair where the plan takes 12 waves (12288 rows; others at a forced split)
-                    assert kname.startswith(("gemm_mfma_pair<3, 1, 2, 12>", "gemm_mfma_round<")), kname
+                else:  # the streaming pair where the plan takes 12 waves (12288 rows; others at a forced split)
+                    assert kname.startswith(("gemm_mfma_pair<3, 1, 2, 12>" if t == 40 else "gemm_mfma_pair<4, 1, 1, 12>", "gemm_mfma_round<")), kname
                     assert kname.startswith("gemm_mfma_pair<") or rows != 12288 or ks, kname
-                else:
-                    assert kname.startswith("gemm_mfma_round<"), kname
                 for g, s1 in zip(got, singles):
                     assert np.array_equal(g.view(np.uint32), s1.view(np.uint32)), (t, ks)
             for g, m in zip(got, mats):
