@@ -760,17 +760,20 @@ def test_random_shapes_every_path(rt, oracle, case):
 
 def random_round_cases(n=14, seed=4242):
     """Seeded rounds: 2 to 8 products sharing x, rows 16..1536 and K 32..4096 columns at random, every
-    third case of one shape (two products of one shape at 5..16 tokens run as a pair), at 1 to 70
-    tokens (decode rounds, x-resident, streaming, and 64-token chunks with a short last one)."""
+    third case of one shape (two products of one shape run as a pair at 5..16 tokens, and at 33..64
+    where the plan takes 12 waves), at 1 to 70 tokens (decode rounds, x-resident, streaming, and
+    64-token chunks with a short last one)."""
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
         k = 2 if i % 3 == 0 else int(rng.integers(2, 9))
         cols = 32 * int(rng.integers(1, 129))
         rows = [16 * int(rng.integers(1, 97)) for _ in range(k)]
-        if i % 3 == 0:
+        if i % 3 == 0:  # one shape: the pair kernels at 5..16 and 33..64 tokens
             rows = [rows[0]] * k
-        t = int(rng.choice([1, 3, 4, 5, 8, 13, 16, 17, 29, 40, 64, 66, 70]))
+            t = int(rng.choice([5, 9, 16, 33, 40, 47, 48, 64, 66]))
+        else:
+            t = int(rng.choice([1, 3, 4, 5, 8, 13, 16, 17, 29, 40, 64, 66, 70]))
         out.append((i, tuple(rows), cols, t))
     return out
 
